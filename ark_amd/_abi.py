@@ -1,0 +1,98 @@
+"""ctypes mirror of the C ABI structs and constants in include/ark_opt.h.
+
+Layouts are checked against the library's own sizeof values
+(`ark_opt_struct_sizes`) when the library is loaded.
+"""
+import ctypes as C
+
+ABI_VERSION = 1
+
+OK = 0
+EARLY_STOP = 1
+EINVAL = -1
+EHIP = -2
+ENOMEM = -3
+
+NORM_SEGMENT = 4096
+
+GRAD_F16 = 0
+GRAD_F32 = 1
+
+TENSOR_NO_UNSCALE = 1
+
+
+class Tensor(C.Structure):
+    _fields_ = [
+        ("w", C.c_void_p),
+        ("g", C.c_void_p),
+        ("m", C.c_void_p),
+        ("v", C.c_void_p),
+        ("n", C.c_uint64),
+        ("weight_decay", C.c_float),
+        ("flags", C.c_uint32),
+    ]
+
+
+class HParams(C.Structure):
+    _fields_ = [
+        ("beta1", C.c_float),
+        ("beta2", C.c_float),
+        ("eps", C.c_float),
+        ("grad_clip", C.c_float),
+        ("loss_scale_init", C.c_float),
+        ("loss_scale_min", C.c_float),
+        ("loss_scale_max", C.c_float),
+        ("scale_up_every", C.c_uint32),
+        ("max_consecutive_nonfinite", C.c_uint32),
+        ("grad_dtype", C.c_uint32),
+    ]
+
+
+class State(C.Structure):
+    _fields_ = [
+        ("t", C.c_uint32),
+        ("loss_scale", C.c_float),
+        ("clean_steps", C.c_uint32),
+        ("consecutive_nonfinite", C.c_uint32),
+        ("skipped_steps", C.c_uint64),
+        ("early_stop", C.c_uint32),
+        ("reserved", C.c_uint32),
+    ]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_ if k != "reserved"}
+
+
+class StepInfo(C.Structure):
+    _fields_ = [
+        ("applied", C.c_int32),
+        ("nonfinite", C.c_int32),
+        ("clipped", C.c_int32),
+        ("status", C.c_int32),
+        ("grad_sumsq", C.c_double),
+        ("grad_norm", C.c_float),
+        ("clip_coef", C.c_float),
+        ("inv_scale", C.c_float),
+        ("lr", C.c_float),
+        ("lr_eff", C.c_float),
+        ("reserved", C.c_float),
+        ("state", State),
+    ]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k, _ in self._fields_ if k not in ("reserved", "state")}
+        d["state"] = self.state.as_dict()
+        return d
+
+
+class Timing(C.Structure):
+    _fields_ = [
+        ("steps", C.c_uint64),
+        ("ms_norm", C.c_double),
+        ("ms_finalize", C.c_double),
+        ("ms_adamw", C.c_double),
+        ("ms_step", C.c_double),
+    ]
+
+
+STRUCTS = (Tensor, HParams, State, StepInfo, Timing)

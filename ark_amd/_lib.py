@@ -1,0 +1,99 @@
+"""Loader of the gfx950 library ark_amd/lib/libark_opt.so (C ABI of
+include/ark_opt.h and include/ark_synth.h).
+
+There is no fallback: if the library is missing or fails to load, every
+caller gets an ImportError-like failure with the reason.
+"""
+import ctypes as C
+import os
+
+from . import _abi
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libark_opt.so")
+CSRC = os.path.join(_HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
+
+_lib = None
+
+
+class ArkOptError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"ark_opt error {code}: {msg}")
+        self.code = code
+
+
+def _declare(L):
+    P = C.c_void_p
+    u64, u32, i32, f32 = C.c_uint64, C.c_uint32, C.c_int32, C.c_float
+    H = C.c_void_p  # opaque handle
+    sig = {
+        "ark_opt_abi_version": ([], C.c_int),
+        "ark_opt_last_error": ([], C.c_char_p),
+        "ark_opt_struct_sizes": ([C.POINTER(C.c_size_t), C.c_int], C.c_int),
+        "ark_opt_default_hparams": ([C.POINTER(_abi.HParams)], C.c_int),
+        "ark_opt_create": ([C.POINTER(_abi.Tensor), i32, C.POINTER(_abi.HParams), P,
+                            C.POINTER(H)], C.c_int),
+        "ark_opt_destroy": ([H], C.c_int),
+        "ark_opt_step": ([H, f32, C.POINTER(_abi.StepInfo)], C.c_int),
+        "ark_opt_record_overflow": ([H, C.POINTER(_abi.StepInfo)], C.c_int),
+        "ark_opt_get_state": ([H, C.POINTER(_abi.State)], C.c_int),
+        "ark_opt_set_state": ([H, C.POINTER(_abi.State)], C.c_int),
+        "ark_opt_set_timing": ([H, C.c_int], C.c_int),
+        "ark_opt_get_timing": ([H, C.POINTER(_abi.Timing)], C.c_int),
+        "ark_hip_adam_step_f16": ([P, P, P, P, u64, f32, f32, f32, f32, f32, u32, P], C.c_int),
+        "ark_synth_normal_f16": ([P, u64, u64, u32, u32, f32, P], C.c_int),
+        "ark_synth_normal_f32": ([P, u64, u64, u32, u32, f32, P], C.c_int),
+        "ark_synth_fill_u16": ([P, u64, C.c_uint16, P], C.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    return sig
+
+
+def lib():
+    """The loaded library (raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+    # torch's wheel carries its own HIP runtime (soname libamdhip64.so.7).  Loading
+    # it first makes this library's libamdhip64.so.7 dependency bind to that same
+    # runtime, so torch's device pointers and streams are valid here; the other
+    # order would put two HIP runtimes in the process.
+    import torch  # noqa: F401
+    L = C.CDLL(LIB_PATH)
+    _declare(L)
+    if L.ark_opt_abi_version() != _abi.ABI_VERSION:
+        raise ImportError("libark_opt ABI version mismatch")
+    sizes = (C.c_size_t * 5)()
+    L.ark_opt_struct_sizes(sizes, 5)
+    for s, st in zip(sizes, _abi.STRUCTS):
+        if s != C.sizeof(st):
+            raise ImportError(f"struct {st.__name__}: C size {s} != ctypes size {C.sizeof(st)}")
+    _lib = L
+    return L
+
+
+def check(rc):
+    """Raise ArkOptError for a negative status; return the status otherwise."""
+    if rc < 0:
+        raise ArkOptError(rc, lib().ark_opt_last_error().decode())
+    return rc
+
+
+def exported_symbols():
+    """Function names declared in include/*.h (every one must be exported)."""
+    import re
+    names = []
+    for h in sorted(os.listdir(INCLUDE)):
+        if not h.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ark_\w+)\s*\(", text, flags=re.M)
+    return names

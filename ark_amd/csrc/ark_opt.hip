@@ -1,0 +1,470 @@
+// ark_opt.hip -- C ABI (include/ark_opt.h) over the gfx950 optimizer-step
+// kernels: handle creation with the device-side tensor table and segment map,
+// the per-step launch sequence, state get/set, timing, and the single-tensor
+// drop-in of ark_asm_adam_step_f16.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "ark_opt_kernels.hpp"
+
+using ark::StepScalars;
+using ark::TensorDev;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(ARK_OPT_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define ARK_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+  } while (0)
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    ok = (prev == dev) || (hipSetDevice(dev) == hipSuccess);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// Host-side bounds check of a caller buffer: it must be device-accessible
+// memory and [p, p + bytes) must lie inside its allocation when the runtime
+// can tell the allocation range.  Catches host pointers and short buffers
+// before any kernel touches them.
+int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
+  if (bytes == 0) return ARK_OPT_OK;
+  if (p == nullptr) return fail(ARK_OPT_EINVAL, "tensor %d: %s is NULL", idx, what);
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is not memory known to HIP", idx,
+                what, p);
+  }
+  if (attr.type == hipMemoryTypeHost && attr.devicePointer == nullptr) {
+    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is host memory", idx, what, p);
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  e = hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p);
+  if (e == hipSuccess && base != nullptr) {
+    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
+    if (q < b || q - b > size || bytes > size - (q - b)) {
+      return fail(ARK_OPT_EINVAL,
+                  "tensor %d: %s [%p, +%llu B) exceeds its allocation [%p, +%zu B)",
+                  idx, what, p, (unsigned long long)bytes, base, size);
+    }
+  } else {
+    (void)hipGetLastError();
+  }
+  return ARK_OPT_OK;
+}
+
+bool finite_f(float x) { return isfinite(x) != 0; }
+
+int check_hparams(const ark_opt_hparams* hp) {
+  if (!hp) return fail(ARK_OPT_EINVAL, "hparams is NULL");
+  if (!finite_f(hp->beta1) || !finite_f(hp->beta2) || !finite_f(hp->eps))
+    return fail(ARK_OPT_EINVAL, "beta1, beta2 and eps must be finite");
+  if (!(hp->grad_clip > 0.0f))  // config.rs:136-138
+    return fail(ARK_OPT_EINVAL, "grad_clip must be > 0 (got %g)", (double)hp->grad_clip);
+  if (!finite_f(hp->loss_scale_init) || !(hp->loss_scale_init > 0.0f))
+    return fail(ARK_OPT_EINVAL, "loss_scale_init must be finite and > 0");
+  if (!(hp->loss_scale_min > 0.0f) || !(hp->loss_scale_max > 0.0f))
+    return fail(ARK_OPT_EINVAL, "loss_scale_min and loss_scale_max must be > 0");
+  if (hp->grad_dtype != ARK_OPT_GRAD_F16 && hp->grad_dtype != ARK_OPT_GRAD_F32)
+    return fail(ARK_OPT_EINVAL, "grad_dtype %u unknown", hp->grad_dtype);
+  return ARK_OPT_OK;
+}
+
+constexpr int kTimingPool = 256;
+
+}  // namespace
+
+struct ark_opt_handle {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  ark_opt_hparams hp{};
+  int32_t ntensors = 0;
+  uint32_t nseg = 0;
+  int spb = 8;
+  uint32_t norm_blocks = 0;
+  uint32_t adam_blocks = 0;
+  // one device allocation carved into the pieces below
+  void* dev_mem = nullptr;
+  TensorDev* d_tab = nullptr;
+  uint32_t* d_seg_tensor = nullptr;
+  double* d_part_sum = nullptr;
+  uint32_t* d_part_flag = nullptr;
+  ark_opt_state* d_state = nullptr;
+  StepScalars* d_scal = nullptr;
+  ark_opt_step_info* d_info = nullptr;
+  ark_opt_step_info* h_info = nullptr;  // pinned
+  ark_opt_state* h_state = nullptr;     // pinned
+  // timing
+  bool timing = false;
+  std::vector<hipEvent_t> ev;  // 4 per pending step
+  int pending = 0;
+  ark_opt_timing acc{};
+};
+
+namespace {
+
+int fold_timing(ark_opt_handle* h) {
+  if (h->pending == 0) return ARK_OPT_OK;
+  ARK_HIP(hipEventSynchronize(h->ev[4 * (h->pending - 1) + 3]));
+  for (int i = 0; i < h->pending; ++i) {
+    hipEvent_t* e = &h->ev[4 * i];
+    float a = 0, b = 0, c = 0, d = 0;
+    ARK_HIP(hipEventElapsedTime(&a, e[0], e[1]));
+    ARK_HIP(hipEventElapsedTime(&b, e[1], e[2]));
+    ARK_HIP(hipEventElapsedTime(&c, e[2], e[3]));
+    ARK_HIP(hipEventElapsedTime(&d, e[0], e[3]));
+    h->acc.ms_norm += a;
+    h->acc.ms_finalize += b;
+    h->acc.ms_adamw += c;
+    h->acc.ms_step += d;
+    h->acc.steps += 1;
+  }
+  h->pending = 0;
+  return ARK_OPT_OK;
+}
+
+void free_handle(ark_opt_handle* h) {
+  if (!h) return;
+  for (hipEvent_t e : h->ev) (void)hipEventDestroy(e);
+  if (h->dev_mem) (void)hipFree(h->dev_mem);
+  if (h->h_info) (void)hipHostFree(h->h_info);
+  if (h->h_state) (void)hipHostFree(h->h_state);
+  delete h;
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+
+extern "C" {
+
+int ark_opt_abi_version(void) { return ARK_OPT_ABI_VERSION; }
+
+const char* ark_opt_last_error(void) { return g_last_error.c_str(); }
+
+int ark_opt_struct_sizes(size_t* out, int n) {
+  const size_t s[5] = {sizeof(ark_opt_tensor), sizeof(ark_opt_hparams),
+                       sizeof(ark_opt_state), sizeof(ark_opt_step_info),
+                       sizeof(ark_opt_timing)};
+  if (!out || n < 0) return fail(ARK_OPT_EINVAL, "out is NULL");
+  int k = n < 5 ? n : 5;
+  for (int i = 0; i < k; ++i) out[i] = s[i];
+  return k;
+}
+
+int ark_opt_default_hparams(ark_opt_hparams* out) {
+  if (!out) return fail(ARK_OPT_EINVAL, "out is NULL");
+  memset(out, 0, sizeof(*out));
+  out->beta1 = 0.9f;                   // optimizer.rs:58
+  out->beta2 = 0.999f;                 // optimizer.rs:59
+  out->eps = 1e-8f;                    // optimizer.rs:60
+  out->grad_clip = 1.0f;               // optimizer.rs:62
+  out->loss_scale_init = 256.0f;       // training.rs:10
+  out->loss_scale_min = 1.0f;          // training.rs:12
+  out->loss_scale_max = 8192.0f;       // config.rs:69
+  out->scale_up_every = 2000u;         // training.rs:13
+  out->max_consecutive_nonfinite = 200u;  // training.rs:235, :298
+  out->grad_dtype = ARK_OPT_GRAD_F16;
+  return ARK_OPT_OK;
+}
+
+int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
+                   const ark_opt_hparams* hp, void* stream,
+                   ark_opt_handle** out) {
+  if (!out) return fail(ARK_OPT_EINVAL, "out is NULL");
+  *out = nullptr;
+  if (!tensors || n_tensors <= 0)
+    return fail(ARK_OPT_EINVAL, "tensor table is empty or NULL (n_tensors=%d)", n_tensors);
+  int rc = check_hparams(hp);
+  if (rc) return rc;
+  const uint64_t gsz = hp->grad_dtype == ARK_OPT_GRAD_F16 ? 2u : 4u;
+
+  // Segment map and host table.
+  std::vector<TensorDev> tab((size_t)n_tensors);
+  std::vector<uint32_t> seg_tensor;
+  uint64_t nseg = 0;
+  for (int32_t i = 0; i < n_tensors; ++i) {
+    const ark_opt_tensor& t = tensors[i];
+    if (t.n > 0) {
+      if (((uintptr_t)t.w & 1u) || ((uintptr_t)t.g & (gsz - 1)) ||
+          ((uintptr_t)t.m & 3u) || ((uintptr_t)t.v & 3u))
+        return fail(ARK_OPT_EINVAL, "tensor %d: pointer not aligned to its element", i);
+      if (!finite_f(t.weight_decay))
+        return fail(ARK_OPT_EINVAL, "tensor %d: weight_decay not finite", i);
+    }
+    TensorDev& d = tab[(size_t)i];
+    d.w = t.w;
+    d.g = t.g;
+    d.m = t.m;
+    d.v = t.v;
+    d.n = t.n;
+    d.wd = t.weight_decay;
+    d.flags = t.flags;
+    d.seg0 = (uint32_t)nseg;
+    d.vec = ((((uintptr_t)t.w | (uintptr_t)t.g | (uintptr_t)t.m | (uintptr_t)t.v) & 15u) == 0) ? 1u : 0u;
+    const uint64_t ns = (t.n + ark::kSeg - 1) / ark::kSeg;
+    if (nseg + ns > 0x7FFFFFFFull)
+      return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)",
+                  (unsigned long long)(nseg + ns));
+    for (uint64_t k = 0; k < ns; ++k) seg_tensor.push_back((uint32_t)i);
+    nseg += ns;
+  }
+  int spb = 8;
+  uint64_t parts = (nseg + 7) / 8;
+  if (parts > ark::kMaxParts) {
+    spb = 16;
+    parts = (nseg + 15) / 16;
+  }
+  if (parts > ark::kMaxParts)
+    return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
+
+  int dev = 0;
+  ARK_HIP(hipGetDevice(&dev));
+  for (int32_t i = 0; i < n_tensors; ++i) {
+    const ark_opt_tensor& t = tensors[i];
+    if ((rc = check_buffer(t.w, t.n * 2u, "w", i))) return rc;
+    if ((rc = check_buffer(t.g, t.n * gsz, "g", i))) return rc;
+    if ((rc = check_buffer(t.m, t.n * 4u, "m", i))) return rc;
+    if ((rc = check_buffer(t.v, t.n * 4u, "v", i))) return rc;
+  }
+
+  ark_opt_handle* h = new ark_opt_handle();
+  h->device = dev;
+  h->stream = (hipStream_t)stream;
+  h->hp = *hp;
+  h->ntensors = n_tensors;
+  h->nseg = (uint32_t)nseg;
+  h->spb = spb;
+  h->norm_blocks = (uint32_t)parts;
+  h->adam_blocks = ark::adamw_blocks((uint32_t)nseg);
+
+  // One allocation: table | seg map | partial sums | flags | state | scalars | info
+  size_t off = 0;
+  const size_t o_tab = off;
+  off = align_up(off + sizeof(TensorDev) * (size_t)n_tensors, 256);
+  const size_t o_seg = off;
+  off = align_up(off + sizeof(uint32_t) * (size_t)(nseg ? nseg : 1), 256);
+  const size_t o_psum = off;
+  off = align_up(off + sizeof(double) * (size_t)(parts ? parts : 1), 256);
+  const size_t o_pflag = off;
+  off = align_up(off + sizeof(uint32_t) * (size_t)(parts ? parts : 1), 256);
+  const size_t o_state = off;
+  off = align_up(off + sizeof(ark_opt_state), 256);
+  const size_t o_scal = off;
+  off = align_up(off + sizeof(StepScalars), 256);
+  const size_t o_info = off;
+  off = align_up(off + sizeof(ark_opt_step_info), 256);
+
+  hipError_t e = hipMalloc(&h->dev_mem, off);
+  if (e != hipSuccess) {
+    free_handle(h);
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMalloc(%zu) failed: %s", off, hipGetErrorString(e));
+  }
+  char* base = (char*)h->dev_mem;
+  h->d_tab = (TensorDev*)(base + o_tab);
+  h->d_seg_tensor = (uint32_t*)(base + o_seg);
+  h->d_part_sum = (double*)(base + o_psum);
+  h->d_part_flag = (uint32_t*)(base + o_pflag);
+  h->d_state = (ark_opt_state*)(base + o_state);
+  h->d_scal = (StepScalars*)(base + o_scal);
+  h->d_info = (ark_opt_step_info*)(base + o_info);
+  if (hipHostMalloc((void**)&h->h_info, sizeof(ark_opt_step_info), hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&h->h_state, sizeof(ark_opt_state), hipHostMallocDefault) != hipSuccess) {
+    free_handle(h);
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipHostMalloc failed");
+  }
+  ark_opt_state st{};
+  st.loss_scale = hp->loss_scale_init;  // training.rs:120
+  StepScalars sc{};
+  e = hipMemcpy(h->d_tab, tab.data(), sizeof(TensorDev) * tab.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess && nseg)
+    e = hipMemcpy(h->d_seg_tensor, seg_tensor.data(), sizeof(uint32_t) * nseg, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(h->d_state, &st, sizeof(st), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(h->d_scal, &sc, sizeof(sc), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    free_handle(h);
+    return hip_fail(e, "uploading the tensor table");
+  }
+  *out = h;
+  return ARK_OPT_OK;
+}
+
+int ark_opt_destroy(ark_opt_handle* h) {
+  if (!h) return ARK_OPT_OK;
+  DeviceGuard g(h->device);
+  (void)hipStreamSynchronize(h->stream);
+  free_handle(h);
+  return ARK_OPT_OK;
+}
+
+static int finish_info(ark_opt_handle* h, ark_opt_step_info* info) {
+  ARK_HIP(hipMemcpyAsync(h->h_info, h->d_info, sizeof(ark_opt_step_info),
+                         hipMemcpyDeviceToHost, h->stream));
+  ARK_HIP(hipStreamSynchronize(h->stream));
+  *info = *h->h_info;
+  return info->status;
+}
+
+int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
+  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
+  if (!finite_f(lr)) return fail(ARK_OPT_EINVAL, "lr must be finite");
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
+  hipEvent_t* ev = nullptr;
+  if (h->timing) {
+    if (h->pending == kTimingPool) {
+      int rc = fold_timing(h);
+      if (rc) return rc;
+    }
+    ev = &h->ev[4 * h->pending];
+    ARK_HIP(hipEventRecord(ev[0], h->stream));
+  }
+  if (h->nseg) {
+    ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_tab,
+                              h->d_seg_tensor, h->nseg, h->d_state, h->d_part_sum,
+                              h->d_part_flag, h->stream));
+  }
+  if (ev) ARK_HIP(hipEventRecord(ev[1], h->stream));
+  ARK_HIP(ark::launch_finalize(h->nseg ? h->norm_blocks : 0u, h->d_part_sum,
+                               h->d_part_flag, h->hp, lr, h->d_state, h->d_scal,
+                               h->d_info, h->stream));
+  if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
+  if (h->nseg) {
+    ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->adam_blocks, h->d_tab,
+                              h->d_seg_tensor, h->nseg, h->d_scal, h->hp.beta1,
+                              h->hp.beta2, h->hp.eps, h->stream));
+  }
+  if (ev) {
+    ARK_HIP(hipEventRecord(ev[3], h->stream));
+    h->pending += 1;
+  }
+  if (info) return finish_info(h, info);
+  return ARK_OPT_OK;
+}
+
+int ark_opt_record_overflow(ark_opt_handle* h, ark_opt_step_info* info) {
+  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
+  ARK_HIP(ark::launch_record_overflow(h->hp, h->d_state, h->d_info, h->stream));
+  if (info) return finish_info(h, info);
+  return ARK_OPT_OK;
+}
+
+int ark_opt_get_state(ark_opt_handle* h, ark_opt_state* out) {
+  if (!h || !out) return fail(ARK_OPT_EINVAL, "handle or out is NULL");
+  DeviceGuard g(h->device);
+  ARK_HIP(hipMemcpyAsync(h->h_state, h->d_state, sizeof(ark_opt_state),
+                         hipMemcpyDeviceToHost, h->stream));
+  ARK_HIP(hipStreamSynchronize(h->stream));
+  *out = *h->h_state;
+  return ARK_OPT_OK;
+}
+
+int ark_opt_set_state(ark_opt_handle* h, const ark_opt_state* st) {
+  if (!h || !st) return fail(ARK_OPT_EINVAL, "handle or state is NULL");
+  if (!finite_f(st->loss_scale) || !(st->loss_scale > 0.0f))
+    return fail(ARK_OPT_EINVAL, "loss_scale must be finite and > 0");
+  DeviceGuard g(h->device);
+  ARK_HIP(hipStreamSynchronize(h->stream));
+  *h->h_state = *st;
+  ARK_HIP(hipMemcpyAsync(h->d_state, h->h_state, sizeof(ark_opt_state),
+                         hipMemcpyHostToDevice, h->stream));
+  ARK_HIP(hipStreamSynchronize(h->stream));
+  return ARK_OPT_OK;
+}
+
+int ark_opt_set_timing(ark_opt_handle* h, int enable) {
+  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
+  DeviceGuard g(h->device);
+  if (enable && h->ev.empty()) {
+    h->ev.resize(4 * kTimingPool);
+    for (auto& e : h->ev) ARK_HIP(hipEventCreate(&e));
+  }
+  if (!enable) {
+    int rc = fold_timing(h);
+    if (rc) return rc;
+  }
+  h->timing = enable != 0;
+  return ARK_OPT_OK;
+}
+
+int ark_opt_get_timing(ark_opt_handle* h, ark_opt_timing* out) {
+  if (!h || !out) return fail(ARK_OPT_EINVAL, "handle or out is NULL");
+  DeviceGuard g(h->device);
+  int rc = fold_timing(h);
+  if (rc) return rc;
+  *out = h->acc;
+  return ARK_OPT_OK;
+}
+
+int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
+                          uint64_t n, float lr, float beta1, float beta2,
+                          float eps, float wd, uint32_t t, void* stream) {
+  if (n == 0) return ARK_OPT_OK;
+  if (((uintptr_t)w & 1u) || ((uintptr_t)g & 3u) || ((uintptr_t)m & 3u) || ((uintptr_t)v & 3u))
+    return fail(ARK_OPT_EINVAL, "pointer not aligned to its element");
+  if (n > 0x7FFFFFFFull * (uint64_t)ark::kSeg)
+    return fail(ARK_OPT_EINVAL, "n too large");
+  int rc;
+  if ((rc = check_buffer(w, n * 2u, "w", 0))) return rc;
+  if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
+  if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;
+  if ((rc = check_buffer(v, n * 4u, "v", 0))) return rc;
+  TensorDev T{};
+  T.w = w;
+  T.g = g;
+  T.m = m;
+  T.v = v;
+  T.n = n;
+  T.wd = wd;
+  T.vec = ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u) == 0) ? 1u : 0u;
+  StepScalars sc{};
+  sc.applied = 1u;
+  sc.inv = 1.0f;
+  sc.coef = 1.0f;
+  sc.lr = lr;
+  sc.lr_eff = ark::lr_eff_of(lr, beta1, beta2, t);  // opti.s:210-258
+  sc.c1 = 1.0f - beta1;                              // opti.s:263-265
+  sc.c2 = 1.0f - beta2;                              // opti.s:266-268
+  ARK_HIP(ark::launch_adamw_single(T, sc, beta1, beta2, eps, (hipStream_t)stream));
+  return ARK_OPT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+// ark_synth.hip -- seeded synthetic inputs on the device (include/ark_synth.h).
+// Integer SplitMix64 counters plus two correctly rounded fp32 multiplies, so a
+// CPU restatement reproduces every bit.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ark_synth.h"
+
+namespace {
+
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__host__ __device__ inline uint64_t synth_base(uint64_t seed, uint32_t tensor_id,
+                                               uint32_t step) {
+  const uint64_t ctr = ((uint64_t)tensor_id << 32) | (uint64_t)step;
+  return mix64(seed + kGolden * (ctr + 1));
+}
+
+__device__ inline float synth_z(uint64_t base, uint64_t i) {
+  const uint64_t x = mix64(base + kGolden * (i + 1));
+  const int32_t u = (int32_t)(x & 0xFFFFu) + (int32_t)((x >> 16) & 0xFFFFu) +
+                    (int32_t)((x >> 32) & 0xFFFFu) + (int32_t)((x >> 48) & 0xFFFFu);
+  const int32_t d = 2 * u - 262140;
+  return (float)d * 0x1.bb67aep-17f;
+}
+
+// fp32 -> fp16 after an fp32 product: the value passes through an empty asm so
+// the compiler cannot merge the multiply and the conversion into one
+// single-rounding mixed-precision fma (the result must be rounded to fp32
+// first, then to fp16).
+__device__ inline uint16_t f32_to_f16_bits(float y) {
+  asm("" : "+v"(y));
+  return __builtin_bit_cast(uint16_t, (_Float16)y);
+}
+
+template <bool kHalf>
+__global__ __launch_bounds__(256) void normal_kernel(void* out, uint64_t n,
+                                                     uint64_t base,
+                                                     float sigma_scale) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float y = synth_z(base, i) * sigma_scale;
+    if constexpr (kHalf)
+      static_cast<uint16_t*>(out)[i] = f32_to_f16_bits(y);
+    else
+      static_cast<float*>(out)[i] = y;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(uint16_t* out, uint64_t n,
+                                                   uint16_t bits) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = bits;
+}
+
+uint32_t grid_for(uint64_t n) {
+  uint64_t b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  return (uint32_t)(b ? b : 1);
+}
+
+int status(hipError_t e) { return e == hipSuccess ? 0 : -2; }
+
+}  // namespace
+
+extern "C" {
+
+int ark_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed,
+                         uint32_t tensor_id, uint32_t step, float sigma_scale,
+                         void* stream) {
+  if (n == 0) return 0;
+  if (!out) return -1;
+  hipLaunchKernelGGL(normal_kernel<true>, dim3(grid_for(n)), dim3(256), 0,
+                     (hipStream_t)stream, (void*)out, n,
+                     synth_base(seed, tensor_id, step), sigma_scale);
+  return status(hipGetLastError());
+}
+
+int ark_synth_normal_f32(float* out, uint64_t n, uint64_t seed,
+                         uint32_t tensor_id, uint32_t step, float sigma_scale,
+                         void* stream) {
+  if (n == 0) return 0;
+  if (!out) return -1;
+  hipLaunchKernelGGL(normal_kernel<false>, dim3(grid_for(n)), dim3(256), 0,
+                     (hipStream_t)stream, (void*)out, n,
+                     synth_base(seed, tensor_id, step), sigma_scale);
+  return status(hipGetLastError());
+}
+
+int ark_synth_fill_u16(uint16_t* out, uint64_t n, uint16_t bits, void* stream) {
+  if (n == 0) return 0;
+  if (!out) return -1;
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0,
+                     (hipStream_t)stream, out, n, bits);
+  return status(hipGetLastError());
+}
+
+}  // extern "C"

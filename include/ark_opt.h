@@ -1,0 +1,201 @@
+/*
+ * ark_opt.h -- C ABI of the MI355X (gfx950) optimizer step for the ARK/EKO
+ * training engine: AMP loss-scale unscale + inf/NaN skip, global L2 gradient
+ * norm, global-norm clipping and the fused fp16-weight / fp32-moment AdamW
+ * update, all as stream-ordered HIP kernels with no host round trip.
+ *
+ * Every entry point is plain C: device pointers, sizes, scalars and an opaque
+ * stream (a hipStream_t passed as void*, NULL = the default stream).  All
+ * functions return an int status (ARK_OPT_OK, ARK_OPT_EARLY_STOP or a negative
+ * error code); nothing aborts.  ark_opt_last_error() gives the message of the
+ * last failure on the calling thread.
+ *
+ * Reference interfaces this replaces (paths relative to proyecto_ark/ark01/):
+ *   asm/opti.s:189-193           ark_asm_adam_step_f16 (per-tensor NEON kernel)
+ *   src/optimizer.rs:44-76       AdamConfig / Optimizer { cfg, step }
+ *   src/optimizer.rs:126-168     Optimizer::clip_all_grads (global L2 clip)
+ *   src/optimizer.rs:171-228     Optimizer::step_all (272 per-tensor calls)
+ *   src/optimizer.rs:237-313     Optimizer::restaurar_momentos (sets step)
+ *   src/training.rs:10-13,54-59  AMP loss-scale constants and state
+ *   src/training.rs:228-241      logits_grad non-finite skip
+ *   src/training.rs:289-326      grad finite check, skip, unscale, step, growth
+ */
+#ifndef ARK_OPT_H
+#define ARK_OPT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARK_OPT_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define ARK_OPT_OK 0
+/* More than max_consecutive_nonfinite skipped steps in a row; mirrors the
+ * Err("early_stop_nan") of training.rs:235-237 and :298-301.  Sticky: every
+ * later step is a no-op that reports it again. */
+#define ARK_OPT_EARLY_STOP 1
+#define ARK_OPT_EINVAL (-1) /* bad argument (null pointer, size, alignment) */
+#define ARK_OPT_EHIP (-2)   /* a HIP runtime call failed */
+#define ARK_OPT_ENOMEM (-3) /* device or pinned allocation failed */
+
+/* ---- norm definition --------------------------------------------------- */
+/* The global sum of squares is a pairwise (index-order binary tree) f64 sum
+ * over the concatenation of every tensor's squared unscaled gradients, each
+ * tensor zero-padded to a multiple of ARK_OPT_NORM_SEGMENT elements and the
+ * whole zero-padded to a power of two.  Any chip, grid or thread count gives
+ * the same bits. */
+#define ARK_OPT_NORM_SEGMENT 4096
+
+/* ---- gradient storage -------------------------------------------------- */
+#define ARK_OPT_GRAD_F16 0u /* fp16 bits, already multiplied by the loss scale */
+#define ARK_OPT_GRAD_F32 1u /* fp32, already multiplied by the loss scale      */
+
+/* ---- per-tensor flags -------------------------------------------------- */
+/* Leave this tensor's gradient scaled (no multiply by 1/loss_scale).  The
+ * reference's scale_grads (training.rs:133-146) skips gamma_final; set this
+ * flag on that tensor to reproduce it bit for bit.  Default: unscale all. */
+#define ARK_OPT_TENSOR_NO_UNSCALE 1u
+
+/* One parameter tensor: the fp16 weight with its gradient and fp32 moments
+ * (memory.rs:202-255: *_fp16 pointer + grad/m/v Tensor).  All pointers are
+ * device memory owned by the caller; the library never frees or reallocates
+ * them.  16-byte aligned pointers take the 128-bit vector path; any other
+ * alignment is accepted and runs element by element. */
+typedef struct ark_opt_tensor {
+  uint16_t *w;        /* fp16 weights, updated in place                    */
+  const void *g;      /* gradients, ark_opt_hparams.grad_dtype, read only  */
+  float *m;           /* first moment, updated in place                    */
+  float *v;           /* second moment, updated in place                   */
+  uint64_t n;         /* elements (0 allowed: the tensor is ignored)        */
+  float weight_decay; /* decoupled wd of this tensor (optimizer.rs:194-226) */
+  uint32_t flags;     /* ARK_OPT_TENSOR_*                                   */
+} ark_opt_tensor;
+
+/* Hyper-parameters fixed for the life of a handle.  AdamConfig fields
+ * (optimizer.rs:44-52) except lr, which is a per-step argument, and
+ * weight_decay, which is per tensor; the AMP scaler constants of
+ * training.rs:10-13 and config.rs:36. */
+typedef struct ark_opt_hparams {
+  float beta1;                        /* optimizer.rs:47                      */
+  float beta2;                        /* optimizer.rs:48                      */
+  float eps;                          /* optimizer.rs:49                      */
+  float grad_clip;                    /* optimizer.rs:50; > 0 (config.rs:136-138),
+                                         INFINITY never clips */
+  float loss_scale_init;              /* training.rs:10 LOSS_SCALE_INIT       */
+  float loss_scale_min;               /* training.rs:12 LOSS_SCALE_MIN        */
+  float loss_scale_max;               /* config.rs:36 loss_scale_max          */
+  uint32_t scale_up_every;            /* training.rs:13 SCALE_UP_EVERY        */
+  uint32_t max_consecutive_nonfinite; /* training.rs:235 and :298 (200)       */
+  uint32_t grad_dtype;                /* ARK_OPT_GRAD_*                       */
+} ark_opt_hparams;
+
+/* Device-resident optimizer + AMP state (Optimizer::step, optimizer.rs:70;
+ * Trainer fields training.rs:54-59).  Read/written with get/set_state. */
+typedef struct ark_opt_state {
+  uint32_t t;                     /* applied AdamW steps ("adam_step")    */
+  float loss_scale;               /* current dynamic loss scale            */
+  uint32_t clean_steps;           /* applied steps since the last change   */
+  uint32_t consecutive_nonfinite; /* skipped steps in a row                */
+  uint64_t skipped_steps;         /* total skipped steps                   */
+  uint32_t early_stop;            /* 1 once the early-stop limit was hit   */
+  uint32_t reserved;
+} ark_opt_state;
+
+/* What one step did.  Filled only when a non-NULL pointer is passed, which
+ * makes the call wait for the step to finish. */
+typedef struct ark_opt_step_info {
+  int32_t applied;    /* 1: AdamW ran; 0: skipped (non-finite or early stop) */
+  int32_t nonfinite;  /* a gradient held inf or NaN                           */
+  int32_t clipped;    /* norm > grad_clip && norm > 0 (optimizer.rs:148)      */
+  int32_t status;     /* ARK_OPT_OK or ARK_OPT_EARLY_STOP                     */
+  double grad_sumsq;  /* f64 sum of squares of the unscaled gradients         */
+  float grad_norm;    /* sqrtf((float)grad_sumsq): pre-clip norm              */
+  float clip_coef;    /* grad_clip / grad_norm when clipped, else 1.0         */
+  float inv_scale;    /* 1.0f / loss_scale used to unscale this step          */
+  float lr;           /* learning rate passed to this step                    */
+  float lr_eff;       /* (sqrtf(bc2) / bc1) * lr (opti.s:255-258)             */
+  float reserved;
+  ark_opt_state state; /* state after the step                                */
+} ark_opt_step_info;
+
+/* Per-kernel device time accumulated while timing is enabled. */
+typedef struct ark_opt_timing {
+  uint64_t steps;     /* steps timed                                   */
+  double ms_norm;     /* total ms in the sum-of-squares / finite kernel */
+  double ms_finalize; /* total ms in the scalar finalize kernel         */
+  double ms_adamw;    /* total ms in the fused AdamW kernel             */
+  double ms_step;     /* total ms from the first to the last kernel     */
+} ark_opt_timing;
+
+typedef struct ark_opt_handle ark_opt_handle;
+
+/* Library ABI version (ARK_OPT_ABI_VERSION).  No reference counterpart. */
+int ark_opt_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *ark_opt_last_error(void);
+
+/* sizeof of each public struct, in the order tensor, hparams, state,
+ * step_info, timing; lets a binding check its layouts.  Returns the count
+ * written (at most n). */
+int ark_opt_struct_sizes(size_t *out, int n);
+
+/* Defaults: AdamConfig::default (optimizer.rs:54-66: beta1 0.9, beta2 0.999,
+ * eps 1e-8, grad_clip 1.0), LOSS_SCALE_INIT 256, LOSS_SCALE_MIN 1,
+ * SCALE_UP_EVERY 2000 (training.rs:10-13), loss_scale_max 8192
+ * (config.rs:69), early stop after 200 (training.rs:235), fp16 gradients. */
+int ark_opt_default_hparams(ark_opt_hparams *out);
+
+/* Optimizer::new (optimizer.rs:74) over a parameter-buffer set.  Copies the
+ * table and its segment map to the device, allocates the workspace and the
+ * device state (t = 0, loss_scale = loss_scale_init), and binds the handle to
+ * `stream` on the current device.  One handle per stream; not thread safe. */
+int ark_opt_create(const ark_opt_tensor *tensors, int32_t n_tensors,
+                   const ark_opt_hparams *hp, void *stream,
+                   ark_opt_handle **out);
+
+int ark_opt_destroy(ark_opt_handle *h);
+
+/* One optimizer step over every tensor: the grad finite check, skip or
+ * unscale, global norm, clip, AdamW with bias correction, and the loss-scale
+ * update of training.rs:289-326 with Optimizer::step_all
+ * (optimizer.rs:171-228).  Stream ordered; with info == NULL nothing waits
+ * on the host.  `lr` is this step's learning rate (Optimizer::lr_now,
+ * optimizer.rs:80-92, evaluated by the caller). */
+int ark_opt_step(ark_opt_handle *h, float lr, ark_opt_step_info *info);
+
+/* The external skip path of training.rs:228-241: the caller found a
+ * non-finite value upstream (the logits gradient) and drops this step.
+ * Halves the scale, counts the skip, may trigger the early stop.  Gradients
+ * and parameters are not touched. */
+int ark_opt_record_overflow(ark_opt_handle *h, ark_opt_step_info *info);
+
+/* Read / overwrite the device state (waits for the stream).  set_state is
+ * the step-restoring half of restaurar_momentos (optimizer.rs:308); the
+ * moments themselves live in the caller's m/v buffers. */
+int ark_opt_get_state(ark_opt_handle *h, ark_opt_state *out);
+int ark_opt_set_state(ark_opt_handle *h, const ark_opt_state *st);
+
+/* Per-kernel timing with HIP events on the handle's stream.  No reference
+ * counterpart (the reference never times its optimizer step). */
+int ark_opt_set_timing(ark_opt_handle *h, int enable);
+int ark_opt_get_timing(ark_opt_handle *h, ark_opt_timing *out);
+
+/* Drop-in for one call of ark_asm_adam_step_f16 (opti.s:189-193, declared
+ * at optimizer.rs:20-23 and ffi.rs:105-108): same arguments in the same
+ * order, fp32 gradients used as given (no unscale, no clip), t == 0 treated
+ * as 1, plus the stream.  Runs the fused AdamW kernel on a one-tensor
+ * table; returns once the work is queued. */
+int ark_hip_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
+                          uint64_t n, float lr, float beta1, float beta2,
+                          float eps, float wd, uint32_t t, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARK_OPT_H */

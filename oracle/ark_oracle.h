@@ -1,0 +1,107 @@
+/*
+ * ark_oracle.h -- TEST INFRASTRUCTURE ONLY.  CPU restatement of the ARK
+ * optimizer-step arithmetic, used as the parity checker by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg.  Nothing in the
+ * product (ark_amd/) links, loads or calls it.
+ *
+ * Sources restated (paths relative to proyecto_ark/ark01/ of the reference):
+ *   asm/opti.s:192-360     per-tensor AdamW, fp16 weights, fp32 g/m/v
+ *   src/optimizer.rs:126-228   global clip + step_all order and per-tensor wd
+ *   src/training.rs:10-13, 228-245, 289-326   AMP scaler state machine
+ *   src/ffi.rs:138-158     vDSP_vsmul = one fp32 multiply per element
+ *
+ * The struct types are the ABI structs of include/ark_opt.h (types only).
+ */
+#ifndef ARK_ORACLE_H
+#define ARK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/ark_opt.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 <-> fp32, software, IEEE binary16 with subnormals, RNE. */
+float ark_ref_f16_to_f32(uint16_t h);
+uint16_t ark_ref_f32_to_f16(float f);
+void ark_ref_f16_to_f32_array(const uint16_t *in, float *out, uint64_t n);
+void ark_ref_f32_to_f16_array(const float *in, uint16_t *out, uint64_t n);
+
+/* Exhaustive cross-checks of the software conversions against the x86 F16C
+ * hardware conversion (vcvtph2ps / vcvtps2ph in RNE).  Return the number of
+ * mismatching inputs (NaNs compare as a class), or -1 without F16C.
+ * f32->f16 covers the inputs [lo, hi) of the 2^32 bit patterns. */
+int64_t ark_ref_check_f16_to_f32_f16c(void);
+int64_t ark_ref_check_f32_to_f16_f16c(uint64_t lo, uint64_t hi, int nthreads);
+
+/* beta^t by the binary exponentiation of opti.s:223-235 (t used as given). */
+float ark_ref_pow_binary(float beta, uint32_t t);
+
+/* Scalar prologue of opti.s:210-271. */
+typedef struct ark_ref_scalars {
+  float decay;  /* 1 - lr*wd            (opti.s:219-221) */
+  float bc1;    /* 1 - beta1^t          (opti.s:223-237) */
+  float bc2;    /* 1 - beta2^t          (opti.s:239-253) */
+  float lr_eff; /* sqrt(bc2)/bc1 * lr   (opti.s:255-258) */
+  float c1;     /* 1 - beta1            (opti.s:263-265) */
+  float c2;     /* 1 - beta2            (opti.s:266-268) */
+} ark_ref_scalars;
+void ark_ref_prologue(float lr, float beta1, float beta2, float wd, uint32_t t,
+                      ark_ref_scalars *out);
+
+/* Exact transliteration of ark_asm_adam_step_f16 (opti.s:192-360). */
+void ark_ref_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
+                           uint64_t n, float lr, float beta1, float beta2,
+                           float eps, float wd, uint32_t t);
+
+/* Canonical f64 sum of squares of the unscaled gradients (see
+ * ARK_OPT_NORM_SEGMENT) and the non-finite flag over a tensor table. */
+double ark_ref_sumsq(const ark_opt_tensor *tab, int32_t nt, uint32_t grad_dtype,
+                     float inv_scale, int nthreads, int32_t *nonfinite);
+
+/* Pairwise (index-order binary tree) f64 sum of x[0..n) zero-padded to a
+ * power of two. */
+double ark_ref_pairwise(const double *x, uint64_t n);
+
+/* Initial state for hparams (t 0, loss_scale_init, counters 0). */
+void ark_ref_state_init(const ark_opt_hparams *hp, ark_opt_state *st);
+
+/* One full fused step (training.rs:289-326 + optimizer.rs:171-228), in
+ * place on the table's w/m/v, with the state machine on *st.  Same return
+ * value and info as ark_opt_step.  nthreads >= 1. */
+int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
+                     const ark_opt_hparams *hp, ark_opt_state *st, float lr,
+                     int nthreads, ark_opt_step_info *info);
+
+/* Same as ark_ref_opt_step but with the global scalars taken from `given`
+ * (applied, clipped, clip_coef, inv_scale, lr_eff from another
+ * implementation's step info) instead of recomputed: the elementwise update
+ * alone.  Used to check elements of a step whose scalars were checked
+ * separately. */
+int ark_ref_apply_given(const ark_opt_tensor *tab, int32_t nt,
+                        const ark_opt_hparams *hp, uint32_t t, float lr,
+                        const ark_opt_step_info *given, int nthreads);
+
+/* training.rs:228-241: external skip. */
+int ark_ref_record_overflow(const ark_opt_hparams *hp, ark_opt_state *st,
+                            ark_opt_step_info *info);
+
+/* Synthetic generator of include/ark_synth.h. */
+uint64_t ark_ref_mix64(uint64_t z);
+uint64_t ark_ref_splitmix64_next(uint64_t *state);
+uint64_t ark_ref_synth_base(uint64_t seed, uint32_t tensor_id, uint32_t step);
+void ark_ref_synth_normal_f32(float *out, uint64_t n, uint64_t seed,
+                              uint32_t tensor_id, uint32_t step,
+                              float sigma_scale);
+void ark_ref_synth_normal_f16(uint16_t *out, uint64_t n, uint64_t seed,
+                              uint32_t tensor_id, uint32_t step,
+                              float sigma_scale);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARK_ORACLE_H */

@@ -1,0 +1,145 @@
+"""TEST INFRASTRUCTURE ONLY: matched GPU / CPU-oracle problems for the parity
+tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+
+A problem is a list of TensorSpec (ark_amd.eko) with seeded inputs built by
+the same counter-based generator on both sides (include/ark_synth.h on the
+GPU, oracle.synth_* on the CPU), so both start from identical bits.
+
+Streams of the generator: weights use (tensor_id = i, step = WEIGHT_STEP);
+gradients of step k use (tensor_id = i, step = k).
+"""
+import numpy as np
+
+import oracle
+from ark_amd import _abi
+
+WEIGHT_STEP = 0xFFFFFFFF
+W_SIGMA = 0.02
+F16_ONE = 0x3C00
+
+
+def f32(x):
+    return float(np.float32(x))
+
+
+def grad_sigma_scale(sigma, loss_scale):
+    """sigma * loss_scale rounded to fp32 (both sides use this value)."""
+    return float(np.float32(np.float32(sigma) * np.float32(loss_scale)))
+
+
+def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
+    """Per-tensor sigma = 10^U(lo, hi), drawn on the host (BASELINE c2)."""
+    rng = np.random.default_rng(seed)
+    return [float(np.float32(10.0 ** rng.uniform(lo, hi))) for _ in range(n)]
+
+
+# ---- host side ----------------------------------------------------------------
+
+def host_problem(specs, seed, weight_decay, sigmas, loss_scale, step=0,
+                 grad_dtype=_abi.GRAD_F16, no_unscale=()):
+    ts = []
+    for i, s in enumerate(specs):
+        if s.gain:
+            w = np.full(s.n, F16_ONE, np.uint16)
+        else:
+            w = oracle.synth_normal_f16(s.n, seed, i, WEIGHT_STEP, W_SIGMA)
+        if grad_dtype == _abi.GRAD_F16:
+            g = oracle.synth_normal_f16(s.n, seed, i, step, grad_sigma_scale(sigmas[i], loss_scale))
+        else:
+            g = oracle.synth_normal_f32(s.n, seed, i, step, grad_sigma_scale(sigmas[i], loss_scale))
+        m = np.zeros(s.n, np.float32)
+        v = np.zeros(s.n, np.float32)
+        ts.append(oracle.HostTensor(w, g, m, v, weight_decay if s.decay else 0.0,
+                                    _abi.TENSOR_NO_UNSCALE if s.name in no_unscale else 0))
+    return ts
+
+
+def host_regen_grads(ts, seed, sigmas, loss_scale, step, grad_dtype=_abi.GRAD_F16):
+    for i, t in enumerate(ts):
+        ss = grad_sigma_scale(sigmas[i], loss_scale)
+        if grad_dtype == _abi.GRAD_F16:
+            t.g[:] = oracle.synth_normal_f16(t.n, seed, i, step, ss)
+        else:
+            t.g[:] = oracle.synth_normal_f32(t.n, seed, i, step, ss)
+
+
+# ---- GPU side -----------------------------------------------------------------
+
+def gpu_problem(specs, seed, weight_decay, sigmas, loss_scale, step=0,
+                grad_dtype=_abi.GRAD_F16, no_unscale=(), device="cuda"):
+    from ark_amd import synth
+    from ark_amd.optimizer import ParamSet
+    ps = ParamSet(specs, weight_decay, device=device, grad_dtype=grad_dtype,
+                  no_unscale=no_unscale)
+    for i, s in enumerate(specs):
+        if s.gain:
+            synth.fill_u16(ps.w(i), F16_ONE)
+        else:
+            synth.normal_f16(ps.w(i), seed, i, WEIGHT_STEP, W_SIGMA)
+    gpu_regen_grads(ps, seed, sigmas, loss_scale, step)
+    return ps
+
+
+def gpu_regen_grads(ps, seed, sigmas, loss_scale, step):
+    from ark_amd import synth
+    for i in range(len(ps)):
+        ss = grad_sigma_scale(sigmas[i], loss_scale)
+        if ps.grad_dtype == _abi.GRAD_F16:
+            synth.normal_f16(ps.g(i), seed, i, step, ss)
+        else:
+            synth.normal_f32(ps.g(i), seed, i, step, ss)
+
+
+def to_host(t):
+    """torch tensor on the GPU -> numpy array with the same bits."""
+    import torch
+    if t.dtype == torch.float16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def compare(ps, ts, idx=None):
+    """Bitwise mismatch counts of w, m, v (NaNs compare equal to NaNs)."""
+    out = {"w": 0, "m": 0, "v": 0, "n": 0}
+    for i in (range(len(ts)) if idx is None else idx):
+        t = ts[i]
+        gw, gm, gv = to_host(ps.w(i)), to_host(ps.m(i)), to_host(ps.v(i))
+        out["w"] += int(np.sum(bits_differ16(gw, t.w)))
+        out["m"] += int(np.sum(bits_differ32(gm, t.m)))
+        out["v"] += int(np.sum(bits_differ32(gv, t.v)))
+        out["n"] += t.n
+    return out
+
+
+def bits_differ16(a, b):
+    a = np.asarray(a, np.uint16)
+    b = np.asarray(b, np.uint16)
+    na = (a & 0x7FFF) > 0x7C00
+    nb = (b & 0x7FFF) > 0x7C00
+    return np.where(na | nb, na != nb, a != b)
+
+
+def bits_differ32(a, b):
+    a = np.asarray(a, np.float32).view(np.uint32)
+    b = np.asarray(b, np.float32).view(np.uint32)
+    na = (a & 0x7FFFFFFF) > 0x7F800000
+    nb = (b & 0x7FFFFFFF) > 0x7F800000
+    return np.where(na | nb, na != nb, a != b)
+
+
+def info_matches(a, b):
+    """Every scalar of two StepInfo structs bit for bit (sumsq included)."""
+    da, db = a.as_dict(), b.as_dict()
+    diffs = {}
+    for k in da:
+        if k == "state":
+            for kk in da[k]:
+                if da[k][kk] != db[k][kk]:
+                    diffs[f"state.{kk}"] = (da[k][kk], db[k][kk])
+        elif isinstance(da[k], float):
+            if np.float64(da[k]).tobytes() != np.float64(db[k]).tobytes() and not (
+                    np.isnan(da[k]) and np.isnan(db[k])):
+                diffs[k] = (da[k], db[k])
+        elif da[k] != db[k]:
+            diffs[k] = (da[k], db[k])
+    return diffs

@@ -1,0 +1,255 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle, bit for
+bit (scalars of every step, every w/m/v element), at BASELINE configs 0 and
+1 and at edge cases of the reference kernel (opti.s:192-360) and the AMP
+state machine (training.rs:289-326)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import harness as H
+from ark_amd import _abi
+from ark_amd.eko import TensorSpec, config_tensors
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return torch
+
+
+def _make(specs, seed, sig, scale, grad_dtype=_abi.GRAD_F16, no_unscale=(), **over):
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    hp = dict(HP)
+    hp.update({k: v for k, v in over.items() if k in hp})
+    amp_kw = {k: v for k, v in over.items() if k in AmpConfig.__dataclass_fields__}
+    cfg = AdamConfig(**hp)
+    amp = AmpConfig(**{"loss_scale_init": scale, "loss_scale_max": 2.0 ** 24, **amp_kw})
+    ps = H.gpu_problem(specs, seed, cfg.weight_decay, sig, scale, grad_dtype=grad_dtype,
+                       no_unscale=no_unscale)
+    ts = H.host_problem(specs, seed, cfg.weight_decay, sig, scale, grad_dtype=grad_dtype,
+                        no_unscale=no_unscale)
+    opt = Optimizer(cfg, ps, amp)
+    ref = oracle.Optimizer(ts, opt.hp, nthreads=8)
+    return cfg, ps, ts, opt, ref
+
+
+def _set_bits(t, pos, bits):
+    """Write fp16 bit pattern `bits` at t[pos] (t: torch.float16 on the GPU)."""
+    import torch
+    t.view(torch.int16)[pos] = int(np.array(bits, np.uint16).view(np.int16))
+
+
+def _run_steps(ps, ts, opt, ref, seed, sig, scale, steps, lr, check_every=1):
+    last = None
+    for k in range(steps):
+        if k:
+            H.gpu_regen_grads(ps, seed, sig, scale, k)
+            H.host_regen_grads(ts, seed, sig, scale, k, grad_dtype=ps.grad_dtype)
+        _, gi = opt.step_all(lr, info=True)
+        _, ri = ref.step(lr)
+        d = H.info_matches(gi, ri)
+        assert not d, f"step {k}: scalars differ: {d}"
+        if (k + 1) % check_every == 0 or k == steps - 1:
+            c = H.compare(ps, ts)
+            assert c["w"] == 0 and c["m"] == 0 and c["v"] == 0, f"step {k}: {c}"
+        last = gi
+    return last
+
+
+def test_synth_generator_matches_oracle():
+    torch = _torch()
+    for n, tid, step, ss in [(1, 0, 0, 1.0), (4099, 3, 17, 0.02), (1 << 20, 271, 4999, 65.536)]:
+        a = torch.empty(n, dtype=torch.float16, device="cuda")
+        from ark_amd import synth
+        synth.normal_f16(a, 1234, tid, step, ss)
+        b = oracle.synth_normal_f16(n, 1234, tid, step, ss)
+        assert np.array_equal(H.to_host(a), b)
+        f = torch.empty(n, dtype=torch.float32, device="cuda")
+        synth.normal_f32(f, 99, tid, step, ss)
+        assert np.array_equal(H.to_host(f).view(np.uint32),
+                              oracle.synth_normal_f32(n, 99, tid, step, ss).view(np.uint32))
+
+
+def test_config0_ten_steps_bit_exact():
+    """BASELINE c0: one 768x768 tensor, grads N(0,1e-3)*1024 fresh per step,
+    10 steps; norm ~0.77 so no clipping."""
+    specs = config_tensors("c0")
+    sig = [1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 11, sig, 1024.0)
+    last = _run_steps(ps, ts, opt, ref, 11, sig, 1024.0, 10, cfg.lr)
+    assert last.state.t == 10 and last.clipped == 0
+    opt.close()
+
+
+def test_config1_layer_hundred_steps_bit_exact():
+    """BASELINE c1: one EKO layer (9 tensors, g1/g2 = 1.0 without wd), 100
+    steps; norm ~2.66 so every step clips."""
+    specs = config_tensors("c1")
+    sig = [1e-3] * len(specs)
+    cfg, ps, ts, opt, ref = _make(specs, 5, sig, 1024.0)
+    last = _run_steps(ps, ts, opt, ref, 5, sig, 1024.0, 100, cfg.lr, check_every=10)
+    assert last.state.t == 100 and last.clipped == 1
+    opt.close()
+
+
+def test_ragged_and_tiny_tensors():
+    specs = [TensorSpec("a", (1,), True, False), TensorSpec("b", (7,), False, True),
+             TensorSpec("c", (4095,), True, False), TensorSpec("d", (4097,), True, False),
+             TensorSpec("e", (8 * 4096 + 13,), True, False), TensorSpec("f", (2048 + 8,), False, False)]
+    sig = [1e-3, 1e-2, 1e-3, 1e-4, 1e-3, 1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 3, sig, 256.0)
+    _run_steps(ps, ts, opt, ref, 3, sig, 256.0, 4, cfg.lr)
+    opt.close()
+
+
+def test_fp32_gradients():
+    specs = [TensorSpec("a", (3000,), True, False), TensorSpec("b", (768,), False, True)]
+    sig = [1e-3, 1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 8, sig, 1000.0, grad_dtype=_abi.GRAD_F32)
+    _run_steps(ps, ts, opt, ref, 8, sig, 1000.0, 3, cfg.lr)
+    opt.close()
+
+
+def test_no_unscale_flag_reproduces_gamma_final_quirk():
+    """training.rs:133-146 leaves gamma_final scaled; the flag reproduces it."""
+    specs = [TensorSpec("embed", (64, 128), True, False),
+             TensorSpec("gamma_final", (128,), False, True)]
+    sig = [1e-3, 1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 4, sig, 512.0, no_unscale=("gamma_final",))
+    last = _run_steps(ps, ts, opt, ref, 4, sig, 512.0, 2, cfg.lr)
+    assert last.clipped == 1  # the scaled gain dominates the norm
+    opt.close()
+
+
+def test_nonfinite_skip_and_recovery():
+    """training.rs:293-305: inf/NaN -> halve the scale, no update, t kept."""
+    torch = _torch()
+    specs = [TensorSpec("a", (5000,), True, False), TensorSpec("b", (768,), False, True)]
+    sig = [1e-3, 1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 9, sig, 65536.0)
+    w0 = H.to_host(ps.w(0)).copy()
+    for bits, ti, pos in [(0x7C00, 0, 4999), (0xFC00, 1, 0), (0x7E01, 0, 1234)]:
+        _set_bits(ps.g(ti), pos, bits)
+        ts[ti].g[pos] = bits
+        _, gi = opt.step_all(cfg.lr, info=True)
+        _, ri = ref.step(cfg.lr)
+        assert not H.info_matches(gi, ri)
+        assert gi.applied == 0 and gi.nonfinite == 1 and gi.state.t == 0
+        H.gpu_regen_grads(ps, 9, sig, 65536.0, 0)
+        H.host_regen_grads(ts, 9, sig, 65536.0, 0)
+    assert np.array_equal(H.to_host(ps.w(0)), w0)
+    assert gi.state.loss_scale == 8192.0 and gi.state.skipped_steps == 3
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert not H.info_matches(gi, ri) and gi.applied == 1 and gi.state.t == 1
+    assert gi.state.consecutive_nonfinite == 0
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0
+    opt.close()
+
+
+def test_growth_cap_and_early_stop():
+    """Growth every scale_up_every clean steps up to the cap with the counter
+    reset even when capped (training.rs:319-326); early stop after more than
+    max_consecutive_nonfinite skips, sticky (training.rs:298-301)."""
+    torch = _torch()
+    specs = [TensorSpec("a", (256,), True, False)]
+    sig = [1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 2, sig, 8.0, scale_up_every=3,
+                                  max_consecutive_nonfinite=4, loss_scale_max=32.0)
+    for k in range(12):
+        _, gi = opt.step_all(cfg.lr, info=True)
+        _, ri = ref.step(cfg.lr)
+        assert not H.info_matches(gi, ri)
+    assert gi.state.loss_scale == 32.0
+    _set_bits(ps.g(0), 7, 0x7C00)
+    ts[0].g[7] = 0x7C00
+    codes = []
+    for k in range(7):
+        rc, gi = opt.step_all(cfg.lr, info=True)
+        rrc, ri = ref.step(cfg.lr)
+        assert rc == rrc and not H.info_matches(gi, ri)
+        codes.append(rc)
+    assert codes == [0, 0, 0, 0, 1, 1, 1]
+    assert gi.state.early_stop == 1 and gi.state.skipped_steps == 5
+    opt.close()
+
+
+def test_record_overflow_matches_oracle():
+    specs = [TensorSpec("a", (512,), True, False)]
+    sig = [1e-3]
+    cfg, ps, ts, opt, ref = _make(specs, 1, sig, 1024.0, max_consecutive_nonfinite=2)
+    for k in range(4):
+        rc, gi = opt.record_overflow()
+        rrc, ri = ref.record_overflow()
+        assert rc == rrc and not H.info_matches(gi, ri)
+    assert gi.state.early_stop == 1
+    opt.close()
+
+
+def test_single_tensor_dropin_matches_reference_kernel():
+    """ark_hip_adam_step_f16 = one ark_asm_adam_step_f16 call (fp32 g, t=0
+    treated as 1, any n, any element alignment)."""
+    torch = _torch()
+    from ark_amd._lib import check, lib
+    rng = np.random.default_rng(0)
+    for n, t, off in [(1, 0, 0), (8, 1, 0), (4096 * 3 + 5, 7, 0), (10000, 123456, 1),
+                      (589824, 2, 0)]:
+        w = oracle.synth_normal_f16(n + off, 3, 0, 0, 0.02)
+        g = (rng.standard_normal(n + off) * 1e-3).astype(np.float32)
+        m = (rng.standard_normal(n + off) * 1e-4).astype(np.float32)
+        v = (rng.random(n + off) * 1e-6).astype(np.float32)
+        dw = torch.from_numpy(w.view(np.int16)).cuda()
+        dg, dm, dv = (torch.from_numpy(a).cuda() for a in (g, m, v))
+        rc = lib().ark_hip_adam_step_f16(
+            dw.data_ptr() + 2 * off, dg.data_ptr() + 4 * off, dm.data_ptr() + 4 * off,
+            dv.data_ptr() + 4 * off, n, 3e-4, 0.9, 0.95, 1e-8, 0.1, t,
+            C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        check(rc)
+        torch.cuda.synchronize()
+        ww, mm, vv = w[off:].copy(), m[off:].copy(), v[off:].copy()
+        oracle.adam_step_f16(ww, g[off:].copy(), mm, vv, 3e-4, 0.9, 0.95, 1e-8, 0.1, t)
+        assert not np.any(H.bits_differ16(dw.cpu().numpy().view(np.uint16)[off:], ww))
+        assert not np.any(H.bits_differ32(dm.cpu().numpy()[off:], mm))
+        assert not np.any(H.bits_differ32(dv.cpu().numpy()[off:], vv))
+
+
+def test_edge_values_weights_near_overflow_and_subnormal_grads():
+    """Weights near 65504 (overflow to inf on requantisation), fp16
+    subnormal weights and gradients, zero gradients."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    n = 4096 + 100
+    specs = [TensorSpec("a", (n,), True, False)]
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 65536, n).astype(np.uint16)
+    w[:64] = np.array([0x7BFF, 0xFBFF, 0x7BFE, 0x0001, 0x8001, 0x03FF, 0x0000, 0x8000] * 8, np.uint16)
+    w[(w & 0x7C00) == 0x7C00] = 0x3C00  # keep weights finite
+    g = rng.integers(0, 0x0400, n).astype(np.uint16) | (rng.integers(0, 2, n).astype(np.uint16) << 15)
+    g[::7] = 0
+    g[100:200] = 0x7BFF  # largest finite gradient
+    # a negative decoupled decay (decay = 1 - lr*wd > 1) pushes weights near
+    # 65504 over the fp16 range
+    cfg = AdamConfig(lr=1e-2, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=-0.1, grad_clip=1e30)
+    amp = AmpConfig(loss_scale_init=1.0)
+    ps = ParamSet(specs, cfg.weight_decay)
+    ps.w(0).copy_(torch.from_numpy(w.view(np.int16)).view(torch.float16))
+    ps.g(0).copy_(torch.from_numpy(g.view(np.int16)).view(torch.float16))
+    ts = [oracle.HostTensor(w.copy(), g.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32),
+                            -0.1)]
+    opt = Optimizer(cfg, ps, amp)
+    ref = oracle.Optimizer(ts, opt.hp)
+    for k in range(3):
+        _, gi = opt.step_all(cfg.lr, info=True)
+        _, ri = ref.step(cfg.lr)
+        assert not H.info_matches(gi, ri)
+        c = H.compare(ps, ts)
+        assert c["w"] == c["m"] == c["v"] == 0, c
+    assert np.any((ts[0].w & 0x7FFF) == 0x7C00)  # some weight overflowed
+    opt.close()
