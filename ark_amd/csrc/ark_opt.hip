@@ -12,8 +12,8 @@
 
 #include "ark_opt_kernels.hpp"
 
+using ark::SegDesc;
 using ark::StepScalars;
-using ark::TensorDev;
 
 namespace {
 
@@ -116,11 +116,9 @@ struct ark_opt_handle {
   uint32_t nseg = 0;
   int spb = 8;
   uint32_t norm_blocks = 0;
-  uint32_t adam_blocks = 0;
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
-  TensorDev* d_tab = nullptr;
-  uint32_t* d_seg_tensor = nullptr;
+  SegDesc* d_segs = nullptr;
   double* d_part_sum = nullptr;
   uint32_t* d_part_flag = nullptr;
   ark_opt_state* d_state = nullptr;
@@ -213,42 +211,42 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   if (rc) return rc;
   const uint64_t gsz = hp->grad_dtype == ARK_OPT_GRAD_F16 ? 2u : 4u;
 
-  // Segment map and host table.
-  std::vector<TensorDev> tab((size_t)n_tensors);
-  std::vector<uint32_t> seg_tensor;
-  uint64_t nseg = 0;
+  // Segment descriptors: every tensor cut into ARK_OPT_NORM_SEGMENT pieces,
+  // tensors in table order, pointers offset to each segment's start.
+  std::vector<SegDesc> segs;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
-    if (t.n > 0) {
-      if (((uintptr_t)t.w & 1u) || ((uintptr_t)t.g & (gsz - 1)) ||
-          ((uintptr_t)t.m & 3u) || ((uintptr_t)t.v & 3u))
-        return fail(ARK_OPT_EINVAL, "tensor %d: pointer not aligned to its element", i);
-      if (!finite_f(t.weight_decay))
-        return fail(ARK_OPT_EINVAL, "tensor %d: weight_decay not finite", i);
-    }
-    TensorDev& d = tab[(size_t)i];
-    d.w = t.w;
-    d.g = t.g;
-    d.m = t.m;
-    d.v = t.v;
-    d.n = t.n;
-    d.wd = t.weight_decay;
-    d.flags = t.flags;
-    d.seg0 = (uint32_t)nseg;
-    d.vec = ((((uintptr_t)t.w | (uintptr_t)t.g | (uintptr_t)t.m | (uintptr_t)t.v) & 15u) == 0) ? 1u : 0u;
+    if (t.n == 0) continue;
+    if (((uintptr_t)t.w & 1u) || ((uintptr_t)t.g & (gsz - 1)) ||
+        ((uintptr_t)t.m & 3u) || ((uintptr_t)t.v & 3u))
+      return fail(ARK_OPT_EINVAL, "tensor %d: pointer not aligned to its element", i);
+    if (!finite_f(t.weight_decay))
+      return fail(ARK_OPT_EINVAL, "tensor %d: weight_decay not finite", i);
     const uint64_t ns = (t.n + ark::kSeg - 1) / ark::kSeg;
-    if (nseg + ns > 0x7FFFFFFFull)
-      return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)",
-                  (unsigned long long)(nseg + ns));
-    for (uint64_t k = 0; k < ns; ++k) seg_tensor.push_back((uint32_t)i);
-    nseg += ns;
+    if (segs.size() + ns > ark::kMaxSegments)
+      return fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %d)",
+                  (unsigned long long)ark::kMaxSegments, ark::kSeg);
+    const bool vec =
+        ((((uintptr_t)t.w | (uintptr_t)t.g | (uintptr_t)t.m | (uintptr_t)t.v) & 15u) == 0);
+    uint32_t flags = vec ? ark::kSegVec : 0u;
+    if (t.flags & ARK_OPT_TENSOR_NO_UNSCALE) flags |= ark::kSegNoUnscale;
+    for (uint64_t k = 0; k < ns; ++k) {
+      const uint64_t off = k * ark::kSeg;
+      SegDesc d;
+      d.w = t.w + off;
+      d.g = (const char*)t.g + off * gsz;
+      d.m = t.m + off;
+      d.v = t.v + off;
+      d.n = (uint32_t)(t.n - off < (uint64_t)ark::kSeg ? t.n - off : (uint64_t)ark::kSeg);
+      d.wd = t.weight_decay;
+      d.flags = flags;
+      d.tensor = (uint32_t)i;
+      segs.push_back(d);
+    }
   }
-  int spb = 8;
-  uint64_t parts = (nseg + 7) / 8;
-  if (parts > ark::kMaxParts) {
-    spb = 16;
-    parts = (nseg + 15) / 16;
-  }
+  const uint64_t nseg = segs.size();
+  const int spb = ark::sumsq_spb(nseg);
+  const uint64_t parts = (nseg + spb - 1) / spb;
   if (parts > ark::kMaxParts)
     return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
 
@@ -270,14 +268,11 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->nseg = (uint32_t)nseg;
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
-  h->adam_blocks = ark::adamw_blocks((uint32_t)nseg);
 
-  // One allocation: table | seg map | partial sums | flags | state | scalars | info
+  // One allocation: segments | partial sums | flags | state | scalars | info
   size_t off = 0;
-  const size_t o_tab = off;
-  off = align_up(off + sizeof(TensorDev) * (size_t)n_tensors, 256);
   const size_t o_seg = off;
-  off = align_up(off + sizeof(uint32_t) * (size_t)(nseg ? nseg : 1), 256);
+  off = align_up(off + sizeof(SegDesc) * (size_t)(nseg ? nseg : 1), 256);
   const size_t o_psum = off;
   off = align_up(off + sizeof(double) * (size_t)(parts ? parts : 1), 256);
   const size_t o_pflag = off;
@@ -296,8 +291,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
     return fail(ARK_OPT_ENOMEM, "hipMalloc(%zu) failed: %s", off, hipGetErrorString(e));
   }
   char* base = (char*)h->dev_mem;
-  h->d_tab = (TensorDev*)(base + o_tab);
-  h->d_seg_tensor = (uint32_t*)(base + o_seg);
+  h->d_segs = (SegDesc*)(base + o_seg);
   h->d_part_sum = (double*)(base + o_psum);
   h->d_part_flag = (uint32_t*)(base + o_pflag);
   h->d_state = (ark_opt_state*)(base + o_state);
@@ -312,9 +306,8 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   ark_opt_state st{};
   st.loss_scale = hp->loss_scale_init;  // training.rs:120
   StepScalars sc{};
-  e = hipMemcpy(h->d_tab, tab.data(), sizeof(TensorDev) * tab.size(), hipMemcpyHostToDevice);
-  if (e == hipSuccess && nseg)
-    e = hipMemcpy(h->d_seg_tensor, seg_tensor.data(), sizeof(uint32_t) * nseg, hipMemcpyHostToDevice);
+  e = hipSuccess;
+  if (nseg) e = hipMemcpy(h->d_segs, segs.data(), sizeof(SegDesc) * nseg, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(h->d_state, &st, sizeof(st), hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(h->d_scal, &sc, sizeof(sc), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -356,9 +349,9 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
     ARK_HIP(hipEventRecord(ev[0], h->stream));
   }
   if (h->nseg) {
-    ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_tab,
-                              h->d_seg_tensor, h->nseg, h->d_state, h->d_part_sum,
-                              h->d_part_flag, h->stream));
+    ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
+                              h->nseg, h->d_state, h->d_part_sum, h->d_part_flag,
+                              h->stream));
   }
   if (ev) ARK_HIP(hipEventRecord(ev[1], h->stream));
   ARK_HIP(ark::launch_finalize(h->nseg ? h->norm_blocks : 0u, h->d_part_sum,
@@ -366,9 +359,8 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
                                h->d_info, h->stream));
   if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
   if (h->nseg) {
-    ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->adam_blocks, h->d_tab,
-                              h->d_seg_tensor, h->nseg, h->d_scal, h->hp.beta1,
-                              h->hp.beta2, h->hp.eps, h->stream));
+    ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->d_segs, h->nseg, h->d_scal,
+                              h->hp.beta1, h->hp.beta2, h->hp.eps, h->stream));
   }
   if (ev) {
     ARK_HIP(hipEventRecord(ev[3], h->stream));
@@ -440,21 +432,15 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   if (n == 0) return ARK_OPT_OK;
   if (((uintptr_t)w & 1u) || ((uintptr_t)g & 3u) || ((uintptr_t)m & 3u) || ((uintptr_t)v & 3u))
     return fail(ARK_OPT_EINVAL, "pointer not aligned to its element");
-  if (n > 0x7FFFFFFFull * (uint64_t)ark::kSeg)
-    return fail(ARK_OPT_EINVAL, "n too large");
+  if ((n + ark::kRow - 1) / ark::kRow * 64u >= (1ull << 32))
+    return fail(ARK_OPT_EINVAL, "n too large (%llu)", (unsigned long long)n);
   int rc;
   if ((rc = check_buffer(w, n * 2u, "w", 0))) return rc;
   if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
   if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;
   if ((rc = check_buffer(v, n * 4u, "v", 0))) return rc;
-  TensorDev T{};
-  T.w = w;
-  T.g = g;
-  T.m = m;
-  T.v = v;
-  T.n = n;
-  T.wd = wd;
-  T.vec = ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u) == 0) ? 1u : 0u;
+  const bool vec =
+      ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u) == 0);
   StepScalars sc{};
   sc.applied = 1u;
   sc.inv = 1.0f;
@@ -463,7 +449,8 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   sc.lr_eff = ark::lr_eff_of(lr, beta1, beta2, t);  // opti.s:210-258
   sc.c1 = 1.0f - beta1;                              // opti.s:263-265
   sc.c2 = 1.0f - beta2;                              // opti.s:266-268
-  ARK_HIP(ark::launch_adamw_single(T, sc, beta1, beta2, eps, (hipStream_t)stream));
+  ARK_HIP(ark::launch_adamw_single(w, g, m, v, n, wd, vec, sc, beta1, beta2, eps,
+                                    (hipStream_t)stream));
   return ARK_OPT_OK;
 }
 

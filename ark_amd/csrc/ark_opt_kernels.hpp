@@ -4,7 +4,7 @@
 //   1. sumsq_kernel   : reads every gradient once (2 B/param for fp16), forms
 //                       the f64 sum of squares of the unscaled gradients along
 //                       the canonical pairwise tree and the inf/NaN flag, one
-//                       partial per block.
+//                       partial per block of SPB segments.
 //   2. finalize_kernel: one block; finishes the tree, runs the AMP skip /
 //                       growth state machine, the clip decision and the bias
 //                       corrections, and writes the step scalars.
@@ -12,11 +12,20 @@
 //                       coefficient, AdamW with decoupled weight decay, fp16
 //                       weight requantisation; exits at once on a skipped step.
 //
-// Tensors are cut into ARK_OPT_NORM_SEGMENT-element segments listed in table
-// order; a block of 256 lanes covers a segment as two halves of 256 x 8
-// elements, lane l owning elements [h*2048 + 8l, h*2048 + 8l + 8) of half h.
-// Every access is a 16-byte load or store when the tensor's pointers are
-// 16-byte aligned and the group of 8 lies inside the tensor.
+// Every tensor is cut into ARK_OPT_NORM_SEGMENT-element segments, listed in
+// table order, each with a 48-byte descriptor holding its four pointers
+// already offset to the segment start, so a block finds its data with one
+// scalar load and no dependent lookups.
+//
+// sumsq_kernel: a 256-lane block covers a segment as two halves of 256 x 8
+// elements, lane l owning elements [h*2048 + 8l, h*2048 + 8l + 8) of half h
+// (one 16-byte load per half).  That layout is what the canonical tree needs:
+// lane groups of 8 in index order.
+// adamw_kernel: one wave per 256-element row, lane l owning elements
+// [4l, 4l + 4): every load and store instruction of every array covers one
+// contiguous span (512 B of fp16, 1 KiB of fp32).  One-wave blocks over a
+// grid of ~a million rows measured fastest on MI355X for this mix of four
+// read streams and three write streams.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,24 +36,29 @@
 namespace ark {
 
 constexpr int kSeg = ARK_OPT_NORM_SEGMENT;  // elements per segment
-constexpr int kBlock = 256;                 // lanes per block (4 waves)
-constexpr int kVec = 8;                     // elements per lane group
+constexpr int kBlock = 256;                 // lanes per sumsq block (4 waves)
+constexpr int kVec = 8;                     // sumsq elements per lane group
 constexpr int kHalfSeg = kBlock * kVec;     // 2048
 static_assert(kSeg == 2 * kHalfSeg, "segment = two halves of 256 x 8");
+constexpr int kRow = 256;                   // adamw elements per wave
+constexpr int kRowsPerSeg = kSeg / kRow;    // 16
 constexpr int kFinThreads = 1024;           // finalize block
 
-// Device copy of one table row.
-struct TensorDev {
-  uint16_t* w;
+// Segment descriptor flags.
+constexpr uint32_t kSegNoUnscale = 1u;  // ARK_OPT_TENSOR_NO_UNSCALE
+constexpr uint32_t kSegVec = 2u;        // w, g, m, v all 16-byte aligned
+
+struct SegDesc {
+  uint16_t* w;      // pointers to the segment's first element
   const void* g;
   float* m;
   float* v;
-  uint64_t n;
-  float wd;
-  uint32_t flags;
-  uint32_t seg0;  // global index of the tensor's first segment
-  uint32_t vec;   // w, g, m, v all 16-byte aligned
+  uint32_t n;       // valid elements in this segment, 1..kSeg
+  float wd;         // weight decay of the tensor
+  uint32_t flags;   // kSeg*
+  uint32_t tensor;  // index in the caller's table
 };
+static_assert(sizeof(SegDesc) == 48, "48-byte descriptor");
 
 // Scalars of one step, written by finalize_kernel, read by adamw_kernel.
 struct StepScalars {
@@ -82,16 +96,21 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
+// Segments per sumsq block (8 or 16) and the resulting partial count.
+int sumsq_spb(uint64_t nseg);
+constexpr uint32_t kMaxParts = 64u * kFinThreads;  // finalize capacity
+// adamw grid: one wave per row, 16 rows per segment; the grid must stay
+// below 2^32 work-items.
+constexpr uint64_t kMaxSegments = (1ull << 32) / (64ull * kRowsPerSeg) - 1;
+
 // ---------------------------------------------------------------------------
-// Kernel entry points (defined in ark_opt_kernels.hip).
+// Launch helpers (ark_opt_kernels.hip); each returns hipSuccess or the error.
 // ---------------------------------------------------------------------------
 
-// Launch helpers return hipSuccess or the launch error.
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
-                        const TensorDev* tab, const uint32_t* seg_tensor,
-                        uint32_t nseg, const ark_opt_state* state,
-                        double* part_sum, uint32_t* part_flag,
-                        hipStream_t stream);
+                        const SegDesc* segs, uint32_t nseg,
+                        const ark_opt_state* state, double* part_sum,
+                        uint32_t* part_flag, hipStream_t stream);
 
 hipError_t launch_finalize(uint32_t nparts, const double* part_sum,
                            const uint32_t* part_flag,
@@ -99,25 +118,20 @@ hipError_t launch_finalize(uint32_t nparts, const double* part_sum,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream);
 
-// Blocks of adamw_kernel for nseg segments.
-uint32_t adamw_blocks(uint32_t nseg);
-
-hipError_t launch_adamw(uint32_t grad_dtype, uint32_t nblocks,
-                        const TensorDev* tab, const uint32_t* seg_tensor,
+hipError_t launch_adamw(uint32_t grad_dtype, const SegDesc* segs,
                         uint32_t nseg, const StepScalars* scal, float beta1,
                         float beta2, float eps, hipStream_t stream);
 
-// One tensor given by value with host-computed scalars (fp32 gradients, no
-// unscale or clip): the drop-in of one ark_asm_adam_step_f16 call.
-hipError_t launch_adamw_single(const TensorDev& t, const StepScalars& sc,
-                               float beta1, float beta2, float eps,
-                               hipStream_t stream);
+// One tensor given by value (fp32 gradients used as given, no unscale or
+// clip) with host-computed scalars: the drop-in of one
+// ark_asm_adam_step_f16 call.  n may exceed one segment.
+hipError_t launch_adamw_single(uint16_t* w, const float* g, float* m, float* v,
+                               uint64_t n, float wd, bool vec,
+                               const StepScalars& sc, float beta1, float beta2,
+                               float eps, hipStream_t stream);
 
 hipError_t launch_record_overflow(const ark_opt_hparams& hp,
                                   ark_opt_state* state,
                                   ark_opt_step_info* info, hipStream_t stream);
-
-// Largest number of block partials finalize_kernel accepts.
-constexpr uint32_t kMaxParts = 64u * kFinThreads;
 
 }  // namespace ark
