@@ -45,6 +45,7 @@ def _declare(L):
         "ark_synth_normal_f16": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_normal_f32": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_fill_u16": ([P, u64, C.c_uint16, P], C.c_int),
+        "ark_synth_copy": ([P, P, u64, P], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -119,8 +119,8 @@ struct ark_opt_handle {
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
-  double* d_part_sum = nullptr;
-  uint32_t* d_part_flag = nullptr;
+  double* d_part_sum = nullptr;  // kFinThreads * fin_leaves, zero past the partials
+  uint32_t fin_leaves = 1;
   ark_opt_state* d_state = nullptr;
   StepScalars* d_scal = nullptr;
   ark_opt_step_info* d_info = nullptr;
@@ -273,10 +273,10 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   size_t off = 0;
   const size_t o_seg = off;
   off = align_up(off + sizeof(SegDesc) * (size_t)(nseg ? nseg : 1), 256);
+  const uint32_t leaves = ark::finalize_leaves((uint32_t)parts);
+  const size_t psum_bytes = sizeof(double) * (size_t)ark::kFinThreads * leaves;
   const size_t o_psum = off;
-  off = align_up(off + sizeof(double) * (size_t)(parts ? parts : 1), 256);
-  const size_t o_pflag = off;
-  off = align_up(off + sizeof(uint32_t) * (size_t)(parts ? parts : 1), 256);
+  off = align_up(off + psum_bytes, 256);
   const size_t o_state = off;
   off = align_up(off + sizeof(ark_opt_state), 256);
   const size_t o_scal = off;
@@ -293,7 +293,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   char* base = (char*)h->dev_mem;
   h->d_segs = (SegDesc*)(base + o_seg);
   h->d_part_sum = (double*)(base + o_psum);
-  h->d_part_flag = (uint32_t*)(base + o_pflag);
+  h->fin_leaves = leaves;
   h->d_state = (ark_opt_state*)(base + o_state);
   h->d_scal = (StepScalars*)(base + o_scal);
   h->d_info = (ark_opt_step_info*)(base + o_info);
@@ -308,6 +308,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   StepScalars sc{};
   e = hipSuccess;
   if (nseg) e = hipMemcpy(h->d_segs, segs.data(), sizeof(SegDesc) * nseg, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(h->d_part_sum, 0, psum_bytes);
   if (e == hipSuccess) e = hipMemcpy(h->d_state, &st, sizeof(st), hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(h->d_scal, &sc, sizeof(sc), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -350,13 +351,11 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
   }
   if (h->nseg) {
     ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
-                              h->nseg, h->d_state, h->d_part_sum, h->d_part_flag,
-                              h->stream));
+                              h->nseg, h->d_state, h->d_part_sum, h->stream));
   }
   if (ev) ARK_HIP(hipEventRecord(ev[1], h->stream));
-  ARK_HIP(ark::launch_finalize(h->nseg ? h->norm_blocks : 0u, h->d_part_sum,
-                               h->d_part_flag, h->hp, lr, h->d_state, h->d_scal,
-                               h->d_info, h->stream));
+  ARK_HIP(ark::launch_finalize(h->fin_leaves, h->d_part_sum, h->hp, lr, h->d_state,
+                               h->d_scal, h->d_info, h->stream));
   if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
   if (h->nseg) {
     ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->d_segs, h->nseg, h->d_scal,

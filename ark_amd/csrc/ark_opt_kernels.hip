@@ -166,11 +166,12 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // Block b covers segments [b*SPB, b*SPB + SPB) and writes the pairwise tree
 // of their 2*SPB half-segment sums: an aligned subtree of the global tree.
+// A block that saw an inf or NaN gradient writes NaN, so the global sum is
+// NaN exactly when some gradient is non-finite (training.rs:291).
 template <typename GT, int SPB>
 __global__ __launch_bounds__(kBlock) void sumsq_kernel(
     const SegDesc* __restrict__ segs, uint32_t nseg,
-    const ark_opt_state* __restrict__ state, double* __restrict__ part_sum,
-    uint32_t* __restrict__ part_flag) {
+    const ark_opt_state* __restrict__ state, double* __restrict__ part_sum) {
   constexpr int V = 2 * SPB;
   static_assert(V <= 64, "one value index per lane of a wave");
   // segments whose loads are in flight together (register budget)
@@ -249,23 +250,24 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
     // pairwise over the V half-segment sums in lane (= index) order
 #pragma unroll
     for (int s = 0; s < log2i(V); ++s) x = x + __shfl_xor(x, 1 << s);
-    if (lane == 0) {
-      part_sum[blockIdx.x] = x;
-      part_flag[blockIdx.x] = any_bad ? 1u : 0u;
-    }
+    if (lane == 0) part_sum[blockIdx.x] = any_bad ? __builtin_nan("") : x;
   }
 }
 
 // ---- kernel 2: finalize ----------------------------------------------------
 
+// Pairwise tree over p[0, L) (p 16-byte aligned, L a power of two).
 template <int L>
-__device__ __forceinline__ double leaf_tree(const double* __restrict__ p,
-                                            uint32_t base, uint32_t n) {
+__device__ __forceinline__ double leaf_tree(const double* __restrict__ p) {
   if constexpr (L == 1) {
-    return base < n ? p[base] : 0.0;
+    return p[0];
+  } else if constexpr (L == 2) {
+    typedef double f64x2 __attribute__((ext_vector_type(2)));
+    const f64x2 v = *(const ARK_GLOBAL f64x2*)p;
+    return v.x + v.y;
   } else {
-    const double a = leaf_tree<L / 2>(p, base, n);
-    const double b = leaf_tree<L / 2>(p, base + L / 2, n);
+    const double a = leaf_tree<L / 2>(p);
+    const double b = leaf_tree<L / 2>(p + L / 2);
     return a + b;
   }
 }
@@ -283,10 +285,10 @@ __device__ inline uint32_t amp_skip(const ark_opt_hparams& hp, ark_opt_state& st
   return ARK_OPT_OK;
 }
 
+// part_sum holds kFinThreads * L partials, zero past the last block's.
 template <int L>
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
-    const double* __restrict__ part_sum, const uint32_t* __restrict__ part_flag,
-    uint32_t nparts, ark_opt_hparams hp, float lr,
+    const double* __restrict__ part_sum, ark_opt_hparams hp, float lr,
     ark_opt_state* __restrict__ state, StepScalars* __restrict__ scal,
     ark_opt_step_info* __restrict__ info) {
   __shared__ double wsum[kFinThreads / 64];
@@ -294,15 +296,10 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const uint32_t base = (uint32_t)tid * L;
-  double x = leaf_tree<L>(part_sum, base, nparts);
-  uint32_t bad = 0;
-#pragma unroll
-  for (int i = 0; i < L; ++i)
-    if (base + i < nparts) bad |= part_flag[base + i];
+  double x = leaf_tree<L>(part_sum + (uint32_t)tid * L);
   x = butterfly_from<0>(x);
   if (lane == 0) wsum[wave] = x;
-  const int any_bad = __syncthreads_or((int)bad);
+  __syncthreads();
   if (wave != 0) return;
   double y = lane < kFinThreads / 64 ? wsum[lane] : 0.0;
 #pragma unroll
@@ -310,6 +307,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   if (lane != 0) return;
 
   const double sumsq = y;
+  const bool any_bad = __builtin_isnan(sumsq);
   ark_opt_state st = *state;
   StepScalars sc = {};
   ark_opt_step_info out = {};
@@ -411,8 +409,7 @@ __device__ __forceinline__ uint32_t adam_elem(uint32_t w16, float g, float& m,
 template <typename GT>
 __device__ __forceinline__ void adam_row(uint16_t* w, const GT* g, float* m, float* v,
                                          uint32_t valid, bool vec, float inv_t,
-                                         uint32_t clipped, float coef,
-                                         const ElemConsts& k) {
+                                         float coef, const ElemConsts& k) {
   const uint32_t e = threadIdx.x * 4u;
   if (vec && valid == (uint32_t)kRow) {
     const typename GradIO<GT>::Raw4 gr = GradIO<GT>::load4(g + e);
@@ -427,8 +424,9 @@ __device__ __forceinline__ void adam_row(uint16_t* w, const GT* g, float* m, flo
     uint32_t wo[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float gj = gf[j] * inv_t;     // training.rs:308
-      if (clipped) gj = gj * coef;  // optimizer.rs:151-165
+      // training.rs:308, then optimizer.rs:151-165 (coef is exactly 1.0f
+      // when the step does not clip, and x * 1.0f == x bit for bit)
+      const float gj = (gf[j] * inv_t) * coef;
       wo[j] = adam_elem(wi[j], gj, mm[j], vv[j], k);
     }
     st_nt<u32x2>(w + e, u32x2{wo[0] | (wo[1] << 16), wo[2] | (wo[3] << 16)});
@@ -439,8 +437,7 @@ __device__ __forceinline__ void adam_row(uint16_t* w, const GT* g, float* m, flo
     for (int j = 0; j < 4; ++j) {
       const uint32_t i = e + j;
       if (i >= valid) break;
-      float gj = GradIO<GT>::load1(g + i, unused) * inv_t;
-      if (clipped) gj = gj * coef;
+      const float gj = (GradIO<GT>::load1(g + i, unused) * inv_t) * coef;
       float mj = ld_g<float>(m + i), vj = ld_g<float>(v + i);
       const uint32_t wj = adam_elem(ld_g<uint16_t>(w + i), gj, mj, vj, k);
       st_g<uint16_t>(w + i, (uint16_t)wj);
@@ -470,7 +467,7 @@ __global__ __launch_bounds__(64) void adamw_kernel(
   c.decay = 1.0f - sc.lr * d.wd;  // opti.s:219-221 with the tensor's wd
   const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : sc.inv;
   adam_row<GT>(d.w + r0, static_cast<const GT*>(d.g) + r0, d.m + r0, d.v + r0, valid,
-               (d.flags & kSegVec) != 0, inv_t, sc.clipped, sc.coef, c);
+               (d.flags & kSegVec) != 0, inv_t, sc.coef, c);
 }
 
 __global__ __launch_bounds__(64) void adamw_single_kernel(
@@ -486,7 +483,7 @@ __global__ __launch_bounds__(64) void adamw_single_kernel(
   c.eps = eps;
   c.lr_eff = sc.lr_eff;
   c.decay = 1.0f - sc.lr * wd;
-  adam_row<float>(w + r0, g + r0, m + r0, v + r0, valid, vec != 0, 1.0f, 0u, 1.0f, c);
+  adam_row<float>(w + r0, g + r0, m + r0, v + r0, valid, vec != 0, 1.0f, 1.0f, c);
 }
 
 }  // namespace
@@ -496,11 +493,11 @@ int sumsq_spb(uint64_t nseg) { return (nseg + 7) / 8 <= kMaxParts ? 8 : 16; }
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
                         const SegDesc* segs, uint32_t nseg,
                         const ark_opt_state* state, double* part_sum,
-                        uint32_t* part_flag, hipStream_t stream) {
+                        hipStream_t stream) {
   const dim3 grid(nblocks), block(kBlock);
 #define ARK_SUMSQ(GT, SPB)                                                        \
   hipLaunchKernelGGL((sumsq_kernel<GT, SPB>), grid, block, 0, stream, segs, nseg, \
-                     state, part_sum, part_flag)
+                     state, part_sum)
   if (grad_dtype == ARK_OPT_GRAD_F16) {
     if (spb == 8) ARK_SUMSQ(uint16_t, 8);
     else ARK_SUMSQ(uint16_t, 16);
@@ -512,24 +509,30 @@ hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
   return hipGetLastError();
 }
 
-hipError_t launch_finalize(uint32_t nparts, const double* part_sum,
-                           const uint32_t* part_flag,
+uint32_t finalize_leaves(uint32_t nparts) {
+  uint32_t L = 1;
+  while ((uint64_t)L * kFinThreads < nparts) L <<= 1;
+  return L;
+}
+
+hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
                            const ark_opt_hparams& hp, float lr,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream) {
   const dim3 grid(1), block(kFinThreads);
-  const uint32_t per = (nparts + kFinThreads - 1) / kFinThreads;
-#define ARK_FIN(L)                                                          \
-  hipLaunchKernelGGL((finalize_kernel<L>), grid, block, 0, stream, part_sum, \
-                     part_flag, nparts, hp, lr, state, scal, info)
-  if (per <= 1) ARK_FIN(1);
-  else if (per <= 2) ARK_FIN(2);
-  else if (per <= 4) ARK_FIN(4);
-  else if (per <= 8) ARK_FIN(8);
-  else if (per <= 16) ARK_FIN(16);
-  else if (per <= 32) ARK_FIN(32);
-  else if (per <= 64) ARK_FIN(64);
-  else return hipErrorInvalidValue;
+#define ARK_FIN(L)                                                                   \
+  hipLaunchKernelGGL((finalize_kernel<L>), grid, block, 0, stream, part_sum, hp, lr, \
+                     state, scal, info)
+  switch (leaves) {
+    case 1: ARK_FIN(1); break;
+    case 2: ARK_FIN(2); break;
+    case 4: ARK_FIN(4); break;
+    case 8: ARK_FIN(8); break;
+    case 16: ARK_FIN(16); break;
+    case 32: ARK_FIN(32); break;
+    case 64: ARK_FIN(64); break;
+    default: return hipErrorInvalidValue;
+  }
 #undef ARK_FIN
   return hipGetLastError();
 }

@@ -107,13 +107,18 @@ constexpr uint64_t kMaxSegments = (1ull << 32) / (64ull * kRowsPerSeg) - 1;
 // Launch helpers (ark_opt_kernels.hip); each returns hipSuccess or the error.
 // ---------------------------------------------------------------------------
 
+// part_sum: one partial per block (NaN when the block saw a non-finite
+// gradient).
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
                         const SegDesc* segs, uint32_t nseg,
                         const ark_opt_state* state, double* part_sum,
-                        uint32_t* part_flag, hipStream_t stream);
+                        hipStream_t stream);
 
-hipError_t launch_finalize(uint32_t nparts, const double* part_sum,
-                           const uint32_t* part_flag,
+// Leaves per finalize thread for nparts partials (a power of two <= 64); the
+// partial buffer must hold kFinThreads * leaves doubles, zero past nparts.
+uint32_t finalize_leaves(uint32_t nparts);
+
+hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
                            const ark_opt_hparams& hp, float lr,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream);

@@ -60,6 +60,18 @@ __global__ __launch_bounds__(256) void fill_kernel(uint16_t* out, uint64_t n,
     out[i] = bits;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst,
+                                                   const u32x4* __restrict__ src,
+                                                   uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i < n)
+    __builtin_nontemporal_store(
+        __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(src + i)),
+        (__attribute__((address_space(1))) u32x4*)(dst + i));
+}
+
 uint32_t grid_for(uint64_t n) {
   uint64_t b = (n + 255) / 256;
   if (b > 65536) b = 65536;
@@ -91,6 +103,17 @@ int ark_synth_normal_f32(float* out, uint64_t n, uint64_t seed,
   hipLaunchKernelGGL(normal_kernel<false>, dim3(grid_for(n)), dim3(256), 0,
                      (hipStream_t)stream, (void*)out, n,
                      synth_base(seed, tensor_id, step), sigma_scale);
+  return status(hipGetLastError());
+}
+
+int ark_synth_copy(void* dst, const void* src, uint64_t nbytes, void* stream) {
+  if (nbytes == 0) return 0;
+  if (!dst || !src || (nbytes & 15u) || (((uintptr_t)dst | (uintptr_t)src) & 15u)) return -1;
+  const uint64_t n = nbytes / 16u;
+  const uint64_t blocks = (n + 255) / 256;
+  if (blocks > 0xFFFFFFFFull / 256u) return -1;
+  hipLaunchKernelGGL(copy_kernel, dim3((uint32_t)blocks), dim3(256), 0,
+                     (hipStream_t)stream, (u32x4*)dst, (const u32x4*)src, n);
   return status(hipGetLastError());
 }
 

@@ -23,6 +23,13 @@ def normal_f32(t, seed, tensor_id, step, sigma_scale):
                                      sigma_scale, _stream(t)))
 
 
+def copy(dst, src):
+    """dst <- src bytes with the library's plain streaming copy kernel."""
+    nbytes = src.numel() * src.element_size()
+    assert dst.is_cuda and src.is_cuda and dst.numel() * dst.element_size() == nbytes
+    check(lib().ark_synth_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream(src)))
+
+
 def fill_u16(t, bits):
     assert t.is_cuda and t.is_contiguous() and t.element_size() == 2
     check(lib().ark_synth_fill_u16(t.data_ptr(), t.numel(), bits, _stream(t)))

@@ -104,6 +104,20 @@ def run_gpu(name, steps, warmup):
     return res
 
 
+def calib_copy(nbytes=1 << 30, reps=3):
+    """A plain copy kernel of known size (ark_synth_copy: one 16-byte
+    non-temporal load and store per thread): under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters."""
+    import torch
+    from ark_amd import synth
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        synth.copy(dst, src)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration copy: {reps} x {nbytes} bytes")
+
+
 def run_cpu_baseline(name, budget_s, threads):
     """The C oracle (same arithmetic, bit-identical results) timed on the
     host cores: full steps of the same workload until budget_s is spent."""
@@ -161,6 +175,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the optimizer step of this build runs on a "
@@ -168,6 +184,8 @@ def main():
         sys.exit(2)
 
     r = run_gpu(a.workload, a.steps, a.warmup)
+    if a.calib_copy:
+        calib_copy()
     n = r["n_params"]
     gbs = BYTES_STEP * n / (r["ms_step"] * 1e-3) / 1e9
     adam_gbs = BYTES_ADAMW * n / (r["ms_adamw"] * 1e-3) / 1e9

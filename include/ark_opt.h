@@ -112,7 +112,8 @@ typedef struct ark_opt_step_info {
   int32_t nonfinite;  /* a gradient held inf or NaN                           */
   int32_t clipped;    /* norm > grad_clip && norm > 0 (optimizer.rs:148)      */
   int32_t status;     /* ARK_OPT_OK or ARK_OPT_EARLY_STOP                     */
-  double grad_sumsq;  /* f64 sum of squares of the unscaled gradients         */
+  double grad_sumsq;  /* f64 sum of squares of the unscaled gradients (NaN
+                         when a gradient is non-finite)                       */
   float grad_norm;    /* sqrtf((float)grad_sumsq): pre-clip norm              */
   float clip_coef;    /* grad_clip / grad_norm when clipped, else 1.0         */
   float inv_scale;    /* 1.0f / loss_scale used to unscale this step          */

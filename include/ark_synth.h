@@ -44,6 +44,13 @@ int ark_synth_normal_f32(float *out, uint64_t n, uint64_t seed,
 /* out[i] = bits for all i (e.g. 0x3C00 = 1.0 for RMSNorm gains). */
 int ark_synth_fill_u16(uint16_t *out, uint64_t n, uint16_t bits, void *stream);
 
+/* Plain device copy of nbytes (a multiple of 16; both pointers 16-byte
+ * aligned) with one 16-byte non-temporal load and store per thread, the
+ * access kind of the optimizer kernels.  Reads and writes exactly nbytes:
+ * the reference point that calibrates byte counters (FETCH_SIZE /
+ * WRITE_SIZE) in profiles. */
+int ark_synth_copy(void *dst, const void *src, uint64_t nbytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

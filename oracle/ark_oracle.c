@@ -502,9 +502,9 @@ int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
   double sumsq =
       ark_ref_sumsq(tab, nt, hp->grad_dtype, inv, nthreads, &nonfinite);
   if (nonfinite) { /* training.rs:293-305: no update, t unchanged */
+    /* the sum of a non-finite step is reported as NaN */
     int status = amp_skip(hp, st);
-    fill_info(info, st, 0, 1, 0, status, sumsq, sqrtf((float)sumsq), 1.0f, inv,
-              lr, 0.0f);
+    fill_info(info, st, 0, 1, 0, status, (double)NAN, NAN, 1.0f, inv, lr, 0.0f);
     return status;
   }
   float norm = sqrtf((float)sumsq);                     /* optimizer.rs:145 */

@@ -76,6 +76,15 @@ def test_synth_generator_matches_oracle():
                               oracle.synth_normal_f32(n, 99, tid, step, ss).view(np.uint32))
 
 
+def test_calibration_copy_kernel():
+    torch = _torch()
+    from ark_amd import synth
+    src = torch.arange(1 << 20, dtype=torch.int32, device="cuda")
+    dst = torch.zeros_like(src)
+    synth.copy(dst, src)
+    assert torch.equal(dst, src)
+
+
 def test_config0_ten_steps_bit_exact():
     """BASELINE c0: one 768x768 tensor, grads N(0,1e-3)*1024 fresh per step,
     10 steps; norm ~0.77 so no clipping."""
