@@ -70,6 +70,8 @@ def lib():
                                       C.c_uint32, C.c_float, C.POINTER(_abi.StepInfo), C.c_int]
     L.ark_ref_record_overflow.argtypes = [C.POINTER(_abi.HParams), C.POINTER(_abi.State),
                                           C.POINTER(_abi.StepInfo)]
+    L.ark_ref_amp_replay.argtypes = [C.POINTER(_abi.HParams), C.POINTER(_abi.State), P,
+                                     C.c_uint64, P]
     L.ark_ref_mix64.argtypes = [C.c_uint64]
     L.ark_ref_mix64.restype = C.c_uint64
     L.ark_ref_splitmix64_next.argtypes = [C.POINTER(C.c_uint64)]
@@ -201,6 +203,26 @@ class Optimizer:
         info = _abi.StepInfo()
         st = lib().ark_ref_record_overflow(C.byref(self.hp), C.byref(self.state), C.byref(info))
         return st, info
+
+
+def amp_replay(hp, state, events):
+    """Run the oracle's AMP state machine over step outcomes (True = skip);
+    returns (status, scales after each step); `state` is updated in place."""
+    ev = np.ascontiguousarray(events, dtype=np.uint8)
+    scales = np.empty(ev.size, np.float32)
+    st = lib().ark_ref_amp_replay(C.byref(hp), C.byref(state), _ptr(ev), ev.size, _ptr(scales))
+    return st, scales
+
+
+def default_hparams():
+    """The reference's defaults (AdamConfig::default, training.rs:10-13,
+    config.rs:69), built here independently of the product library."""
+    hp = _abi.HParams()
+    hp.beta1, hp.beta2, hp.eps, hp.grad_clip = 0.9, 0.999, 1e-8, 1.0
+    hp.loss_scale_init, hp.loss_scale_min, hp.loss_scale_max = 256.0, 1.0, 8192.0
+    hp.scale_up_every, hp.max_consecutive_nonfinite = 2000, 200
+    hp.grad_dtype = _abi.GRAD_F16
+    return hp
 
 
 # ---- generator ---------------------------------------------------------------

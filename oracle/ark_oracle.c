@@ -488,6 +488,37 @@ static int amp_skip(const ark_opt_hparams *hp, ark_opt_state *st) {
   return ARK_OPT_OK;
 }
 
+/* Clean-step bookkeeping after an applied update (training.rs:316-326);
+ * `scale` is the scale the step ran with. */
+static void amp_clean(const ark_opt_hparams *hp, ark_opt_state *st, float scale) {
+  st->clean_steps += 1;                                    /* :317 */
+  st->consecutive_nonfinite = 0;                           /* :318 */
+  if (st->clean_steps >= hp->scale_up_every) {             /* :319 */
+    float nueva = fminf(scale * 2.0f, hp->loss_scale_max); /* :320 */
+    if (nueva > scale) st->loss_scale = nueva;             /* :321-324 */
+    st->clean_steps = 0;                                   /* :325 */
+  }
+}
+
+int ark_ref_amp_replay(const ark_opt_hparams *hp, ark_opt_state *st,
+                       const uint8_t *events, uint64_t n, float *scale_out) {
+  int status = ARK_OPT_OK;
+  for (uint64_t i = 0; i < n; ++i) {
+    if (st->early_stop) {
+      status = ARK_OPT_EARLY_STOP;
+    } else if (events[i]) {
+      status = amp_skip(hp, st);
+    } else {
+      float scale = st->loss_scale;
+      st->t += 1; /* optimizer.rs:172 */
+      amp_clean(hp, st, scale);
+      status = ARK_OPT_OK;
+    }
+    if (scale_out) scale_out[i] = st->loss_scale;
+  }
+  return status;
+}
+
 int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
                      const ark_opt_hparams *hp, ark_opt_state *st, float lr,
                      int nthreads, ark_opt_step_info *info) {
@@ -514,13 +545,7 @@ int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
   ark_ref_scalars s0;
   ark_ref_prologue(lr, hp->beta1, hp->beta2, 0.0f, st->t, &s0);
   run_update(tab, nt, hp, st->t, lr, inv, clipped, coef, nthreads);
-  st->clean_steps += 1;                                  /* training.rs:317 */
-  st->consecutive_nonfinite = 0;                         /* :318 */
-  if (st->clean_steps >= hp->scale_up_every) {           /* :319 */
-    float nueva = fminf(scale * 2.0f, hp->loss_scale_max); /* :320 */
-    if (nueva > scale) st->loss_scale = nueva;            /* :321-324 */
-    st->clean_steps = 0;                                  /* :325 */
-  }
+  amp_clean(hp, st, scale); /* training.rs:316-326 */
   fill_info(info, st, 1, 0, clipped, ARK_OPT_OK, sumsq, norm, coef, inv, lr,
             s0.lr_eff);
   return ARK_OPT_OK;

@@ -85,6 +85,13 @@ int ark_ref_apply_given(const ark_opt_tensor *tab, int32_t nt,
                         const ark_opt_hparams *hp, uint32_t t, float lr,
                         const ark_opt_step_info *given, int nthreads);
 
+/* The AMP state machine alone over a sequence of step outcomes: events[i]
+ * nonzero = a non-finite step (skip), zero = an applied step.  Runs the same
+ * bookkeeping code as ark_ref_opt_step; scale_out[i] (optional) receives the
+ * loss scale after step i.  Returns the last step's status. */
+int ark_ref_amp_replay(const ark_opt_hparams *hp, ark_opt_state *st,
+                       const uint8_t *events, uint64_t n, float *scale_out);
+
 /* training.rs:228-241: external skip. */
 int ark_ref_record_overflow(const ark_opt_hparams *hp, ark_opt_state *st,
                             ark_opt_step_info *info);
