@@ -1,0 +1,111 @@
+"""The C ABI library on the CPU (no GPU calls): it loads, exports every
+function include/*.h declares with matching struct layouts, and rejects bad
+arguments before touching the device."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from ark_amd import _abi
+from ark_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _lib.exported_symbols()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(L, n), n
+    # and the header list is complete: every ark_* symbol of the .so is declared
+    syms = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = set(re.findall(r" T (ark_\w+)", syms))
+    assert exported == set(names)
+
+
+def test_struct_layouts_match():
+    L = _lib.lib()
+    sizes = (C.c_size_t * 5)()
+    assert L.ark_opt_struct_sizes(sizes, 5) == 5
+    assert list(sizes) == [C.sizeof(s) for s in _abi.STRUCTS]
+    assert L.ark_opt_abi_version() == _abi.ABI_VERSION
+    assert L.ark_opt_struct_sizes(None, 5) == _abi.EINVAL
+
+
+def _hp():
+    hp = _abi.HParams()
+    _lib.lib().ark_opt_default_hparams(C.byref(hp))
+    return hp
+
+
+def _create(table, n, hp):
+    h = C.c_void_p()
+    rc = _lib.lib().ark_opt_create(table, n, C.byref(hp) if hp is not None else None, None,
+                                   C.byref(h))
+    return rc, h, _lib.lib().ark_opt_last_error().decode()
+
+
+def test_create_rejects_bad_arguments_before_device_calls():
+    t = (_abi.Tensor * 1)()
+    t[0].w, t[0].g, t[0].m, t[0].v, t[0].n = 0x1000, 0x2000, 0x3000, 0x4000, 10
+    assert _create(None, 1, _hp())[0] == _abi.EINVAL
+    assert _create(t, 0, _hp())[0] == _abi.EINVAL
+    rc, h, msg = _create(t, 1, None)
+    assert rc == _abi.EINVAL and "hparams" in msg
+    for field, value, word in [("grad_clip", 0.0, "grad_clip"), ("grad_clip", -1.0, "grad_clip"),
+                               ("grad_clip", float("nan"), "grad_clip"),
+                               ("beta1", float("nan"), "finite"),
+                               ("loss_scale_init", float("inf"), "loss_scale_init"),
+                               ("loss_scale_min", 0.0, "loss_scale_min"),
+                               ("grad_dtype", 7, "grad_dtype")]:
+        hp = _hp()
+        setattr(hp, field, value)
+        rc, h, msg = _create(t, 1, hp)
+        assert rc == _abi.EINVAL and word in msg, (field, msg)
+    t[0].w = 0x1001  # odd address for fp16
+    rc, h, msg = _create(t, 1, _hp())
+    assert rc == _abi.EINVAL and "aligned" in msg
+    t[0].w = 0x1000
+    t[0].weight_decay = float("nan")
+    rc, h, msg = _create(t, 1, _hp())
+    assert rc == _abi.EINVAL and "weight_decay" in msg
+
+
+def test_single_tensor_dropin_argument_checks():
+    L = _lib.lib()
+    assert L.ark_hip_adam_step_f16(None, None, None, None, 0, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1,
+                                   None) == _abi.OK
+    rc = L.ark_hip_adam_step_f16(0x1001, 0x2000, 0x3000, 0x4000, 10, 3e-4, 0.9, 0.999, 1e-8,
+                                 0.01, 1, None)
+    assert rc == _abi.EINVAL
+    rc = L.ark_hip_adam_step_f16(0x1000, 0x2002, 0x3000, 0x4000, 10, 3e-4, 0.9, 0.999, 1e-8,
+                                 0.01, 1, None)
+    assert rc == _abi.EINVAL
+
+
+def test_synth_argument_checks():
+    L = _lib.lib()
+    assert L.ark_synth_copy(0x1000, 0x2008, 64, None) == -1
+    assert L.ark_synth_copy(0x1000, 0x2000, 17, None) == -1
+    assert L.ark_synth_copy(None, None, 0, None) == 0
+    assert L.ark_synth_normal_f16(None, 0, 1, 2, 3, 1.0, None) == 0
+    assert L.ark_synth_normal_f16(None, 5, 1, 2, 3, 1.0, None) == -1
+
+
+def test_handle_calls_reject_null():
+    L = _lib.lib()
+    assert L.ark_opt_step(None, 1e-3, None) == _abi.EINVAL
+    assert L.ark_opt_record_overflow(None, None) == _abi.EINVAL
+    assert L.ark_opt_get_state(None, None) == _abi.EINVAL
+    assert L.ark_opt_set_state(None, None) == _abi.EINVAL
+    assert L.ark_opt_destroy(None) == _abi.OK
+
+
+def test_headers_cite_reference_interfaces():
+    text = open(os.path.join(ROOT, "include", "ark_opt.h")).read()
+    for cite in ("opti.s:189-193", "optimizer.rs:171-228", "training.rs:289-326",
+                 "training.rs:228-241", "optimizer.rs:237-313"):
+        assert cite in text

@@ -1,0 +1,135 @@
+"""Pins of the oracle's global gradient norm and finite check
+(Optimizer::clip_all_grads, optimizer.rs:126-168; training.rs:291).
+
+The sum of squares is defined as a pairwise f64 tree (include/ark_opt.h,
+ARK_OPT_NORM_SEGMENT) instead of the reference's sequential f32 fold, which
+is off by far more than the 1e-5 the north star allows at EKO sizes (shown
+below).  Pinned here by exact sums (math.fsum), an independent numpy build
+of the tree, exact special cases and invariants."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from ark_amd import _abi
+
+SEG = _abi.NORM_SEGMENT
+
+
+def _tensors(gs, flags=None):
+    out = []
+    for i, g in enumerate(gs):
+        n = g.size
+        out.append(oracle.HostTensor(np.zeros(n, np.uint16), g, np.zeros(n, np.float32),
+                                     np.zeros(n, np.float32), 0.0,
+                                     (flags or [0] * len(gs))[i]))
+    return out
+
+
+def _np_canonical(gs, inv, dtype=_abi.GRAD_F16, flags=None):
+    """Independent numpy build of the canonical tree: per-tensor padding to a
+    multiple of the segment, concatenation, padding to a power of two, then
+    repeated adjacent-pair sums."""
+    parts = []
+    for i, g in enumerate(gs):
+        f = g.view(np.float16).astype(np.float32) if dtype == _abi.GRAD_F16 else g
+        s = np.float32(1.0) if (flags and flags[i]) else np.float32(inv)
+        q = (f * s).astype(np.float64) ** 2
+        pad = (-q.size) % SEG
+        parts.append(np.concatenate([q, np.zeros(pad)]))
+    x = np.concatenate(parts) if parts else np.zeros(1)
+    p = 1
+    while p < x.size:
+        p *= 2
+    x = np.concatenate([x, np.zeros(p - x.size)])
+    while x.size > 1:
+        x = x[0::2] + x[1::2]
+    return float(x[0])
+
+
+def _f16(rng, n, scale):
+    return (rng.standard_normal(n) * scale).astype(np.float16).view(np.uint16)
+
+
+def test_pairwise_tree_shape():
+    """Pairwise, not sequential: ((1 + e) + (e + e)) with e = 2^-53 keeps
+    2^-52, a left fold loses it."""
+    e = 2.0 ** -53
+    assert oracle.pairwise(np.array([1.0, e, e, e])) == 1.0 + 2 * e
+    assert ((1.0 + e) + e) + e == 1.0
+    assert oracle.pairwise(np.array([3.0])) == 3.0
+    assert oracle.pairwise(np.arange(1000, dtype=np.float64)) == 999 * 1000 / 2
+
+
+def test_sumsq_matches_independent_tree():
+    rng = np.random.default_rng(1)
+    sizes = [1, 7, 768, 4095, 4096, 4097, 3 * 4096 + 5, 70000]
+    gs = [_f16(rng, n, 10.0 ** rng.uniform(-3, 1)) for n in sizes]
+    for inv in (1.0, 1.0 / 1024, 1.0 / 65536, 1.0 / 3):
+        got, bad = oracle.sumsq(_tensors(gs), _abi.GRAD_F16, inv, nthreads=4)
+        assert not bad
+        assert got == _np_canonical(gs, inv)
+
+
+def test_sumsq_close_to_exact_sum():
+    rng = np.random.default_rng(2)
+    gs = [_f16(rng, n, 1e3) for n in (589824, 1572864, 768)]
+    got, _ = oracle.sumsq(_tensors(gs), _abi.GRAD_F16, 1.0 / 65536, nthreads=8)
+    exact = math.fsum(float(x) ** 2 for g in gs
+                      for x in (g.view(np.float16).astype(np.float32) * np.float32(1 / 65536)))
+    assert abs(got - exact) <= 1e-13 * exact
+
+
+def test_exact_special_cases():
+    one_hot = np.zeros(10000, np.uint16)
+    one_hot[4321] = np.array([3.0], np.float16).view(np.uint16)[0]
+    assert oracle.sumsq(_tensors([one_hot]), _abi.GRAD_F16, 1.0)[0] == 9.0
+    ones = np.full(12345, 0x3C00, np.uint16)
+    assert oracle.sumsq(_tensors([ones]), _abi.GRAD_F16, 1.0)[0] == 12345.0
+    # power-of-two unscale commutes exactly with the tree
+    rng = np.random.default_rng(3)
+    g = _f16(rng, 50000, 100.0)
+    a = oracle.sumsq(_tensors([g]), _abi.GRAD_F16, 1.0)[0]
+    b = oracle.sumsq(_tensors([g]), _abi.GRAD_F16, 1.0 / 256)[0]
+    assert b == a / 65536.0
+
+
+def test_no_unscale_flag_and_fp32_gradients():
+    rng = np.random.default_rng(4)
+    gs = [_f16(rng, 5000, 1.0), _f16(rng, 768, 1.0)]
+    flags = [0, _abi.TENSOR_NO_UNSCALE]
+    got = oracle.sumsq(_tensors(gs, flags), _abi.GRAD_F16, 1 / 512)[0]
+    assert got == _np_canonical(gs, 1 / 512, flags=flags)
+    g32 = [(rng.standard_normal(n) * 3).astype(np.float32) for n in (100, 9000)]
+    got = oracle.sumsq(_tensors(g32), _abi.GRAD_F32, 1 / 1000)[0]
+    assert got == _np_canonical(g32, 1 / 1000, dtype=_abi.GRAD_F32)
+
+
+def test_finite_flag_exhaustive_over_fp16():
+    pats = np.arange(65536, dtype=np.uint16)
+    bad_expected = (pats & 0x7C00) == 0x7C00  # exponent all ones: inf or NaN
+    for p in (0x0000, 0x3C00, 0x7BFF, 0x8001, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFFFF):
+        t = np.array([0x3C00] * 10 + [p], np.uint16)
+        assert oracle.sumsq(_tensors([t]), _abi.GRAD_F16, 1.0)[1] == bool(bad_expected[p])
+    finite = pats[~bad_expected]
+    assert not oracle.sumsq(_tensors([finite]), _abi.GRAD_F16, 1.0)[1]
+    for p in pats[bad_expected][::17]:
+        t = finite.copy()
+        t[12345] = p
+        assert oracle.sumsq(_tensors([t]), _abi.GRAD_F16, 1.0)[1]
+
+
+def test_reference_sequential_f32_norm_misses_1e5_at_embedding_size():
+    """The reference sums squares with a sequential f32 fold per tensor
+    (optimizer.rs:130-143).  At the EKO embedding size (32000 x 768) that
+    fold is ~1e-2 off, so the 1e-5 norm tolerance is only meetable against an
+    f64-accumulated definition."""
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(32000 * 768) * 1e-3).astype(np.float32)
+    seq = np.cumsum(g * g, dtype=np.float32)[-1]  # left fold in f32
+    exact = float(np.sum(g.astype(np.float64) ** 2))
+    assert abs(float(seq) - exact) / exact > 1e-3
+    t = _tensors([g])
+    got = oracle.sumsq(t, _abi.GRAD_F32, 1.0, nthreads=8)[0]
+    assert abs(got - exact) / exact < 1e-12
