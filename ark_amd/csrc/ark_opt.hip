@@ -68,8 +68,12 @@ int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
     return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is not memory known to HIP", idx,
                 what, p);
   }
-  if (attr.type == hipMemoryTypeHost && attr.devicePointer == nullptr) {
-    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is host memory", idx, what, p);
+  const bool device_ok = attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged ||
+                         attr.type == hipMemoryTypeArray || attr.type == hipMemoryTypeUnified ||
+                         (attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr);
+  if (!device_ok) {
+    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is host memory the device cannot access",
+                idx, what, p);
   }
   hipDeviceptr_t base = nullptr;
   size_t size = 0;

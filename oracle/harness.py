@@ -35,10 +35,19 @@ def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
 
 # ---- host side ----------------------------------------------------------------
 
+def _pmap(fn, items, nthreads):
+    """Map over items on a thread pool (the oracle's C calls release the GIL)."""
+    if nthreads <= 1:
+        return [fn(x) for x in items]
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(nthreads) as ex:
+        return list(ex.map(fn, items))
+
+
 def host_problem(specs, seed, weight_decay, sigmas, loss_scale, step=0,
-                 grad_dtype=_abi.GRAD_F16, no_unscale=()):
-    ts = []
-    for i, s in enumerate(specs):
+                 grad_dtype=_abi.GRAD_F16, no_unscale=(), nthreads=1):
+    def make(i):
+        s = specs[i]
         if s.gain:
             w = np.full(s.n, F16_ONE, np.uint16)
         else:
@@ -49,18 +58,21 @@ def host_problem(specs, seed, weight_decay, sigmas, loss_scale, step=0,
             g = oracle.synth_normal_f32(s.n, seed, i, step, grad_sigma_scale(sigmas[i], loss_scale))
         m = np.zeros(s.n, np.float32)
         v = np.zeros(s.n, np.float32)
-        ts.append(oracle.HostTensor(w, g, m, v, weight_decay if s.decay else 0.0,
-                                    _abi.TENSOR_NO_UNSCALE if s.name in no_unscale else 0))
-    return ts
+        return oracle.HostTensor(w, g, m, v, weight_decay if s.decay else 0.0,
+                                 _abi.TENSOR_NO_UNSCALE if s.name in no_unscale else 0)
+    return _pmap(make, range(len(specs)), nthreads)
 
 
-def host_regen_grads(ts, seed, sigmas, loss_scale, step, grad_dtype=_abi.GRAD_F16):
-    for i, t in enumerate(ts):
+def host_regen_grads(ts, seed, sigmas, loss_scale, step, grad_dtype=_abi.GRAD_F16,
+                     nthreads=1):
+    def regen(i):
+        t = ts[i]
         ss = grad_sigma_scale(sigmas[i], loss_scale)
         if grad_dtype == _abi.GRAD_F16:
             t.g[:] = oracle.synth_normal_f16(t.n, seed, i, step, ss)
         else:
             t.g[:] = oracle.synth_normal_f32(t.n, seed, i, step, ss)
+    _pmap(regen, range(len(ts)), nthreads)
 
 
 # ---- GPU side -----------------------------------------------------------------
@@ -98,16 +110,23 @@ def to_host(t):
     return t.cpu().numpy()
 
 
-def compare(ps, ts, idx=None):
+def compare(ps, ts, idx=None, nthreads=1):
     """Bitwise mismatch counts of w, m, v (NaNs compare equal to NaNs)."""
     out = {"w": 0, "m": 0, "v": 0, "n": 0}
-    for i in (range(len(ts)) if idx is None else idx):
+    idx = list(range(len(ts)) if idx is None else idx)
+    host = [(to_host(ps.w(i)), to_host(ps.m(i)), to_host(ps.v(i))) for i in idx]
+
+    def count(k):
+        i = idx[k]
+        gw, gm, gv = host[k]
         t = ts[i]
-        gw, gm, gv = to_host(ps.w(i)), to_host(ps.m(i)), to_host(ps.v(i))
-        out["w"] += int(np.sum(bits_differ16(gw, t.w)))
-        out["m"] += int(np.sum(bits_differ32(gm, t.m)))
-        out["v"] += int(np.sum(bits_differ32(gv, t.v)))
-        out["n"] += t.n
+        return (int(np.sum(bits_differ16(gw, t.w))), int(np.sum(bits_differ32(gm, t.m))),
+                int(np.sum(bits_differ32(gv, t.v))), t.n)
+    for w, m, v, n in _pmap(count, range(len(idx)), nthreads):
+        out["w"] += w
+        out["m"] += m
+        out["v"] += v
+        out["n"] += n
     return out
 
 

@@ -1,0 +1,183 @@
+"""GPU parity at BASELINE's full sizes: the EKO-237M set (c2), its 5000-step
+AMP stress trajectory (c3) and the 1.3B scale-up (c4), checked against the
+CPU oracle bit for bit (every scalar and every w/m/v element of the steps
+run), plus the state/restore and timing entry points."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import harness as H
+from ark_amd import _abi
+from ark_amd.eko import config_tensors
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def _opt(ps, scale, **amp_kw):
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    cfg = AdamConfig(**HP)
+    amp = AmpConfig(**{"loss_scale_init": scale, "loss_scale_max": 2.0 ** 24, **amp_kw})
+    return cfg, Optimizer(cfg, ps, amp)
+
+
+def _full_size_steps(name, sig, scale, steps, seed):
+    specs = config_tensors(name)
+    from ark_amd.optimizer import AdamConfig
+    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, scale)
+    cfg, opt = _opt(ps, scale)
+    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, scale, nthreads=THREADS)
+    ref = oracle.Optimizer(ts, opt.hp, nthreads=THREADS)
+    infos = []
+    for k in range(steps):
+        if k:
+            H.gpu_regen_grads(ps, seed, sig, scale, k)
+            H.host_regen_grads(ts, seed, sig, scale, k, nthreads=THREADS)
+        _, gi = opt.step_all(cfg.lr, info=True)
+        _, ri = ref.step(cfg.lr)
+        assert not H.info_matches(gi, ri), (k, H.info_matches(gi, ri))
+        c = H.compare(ps, ts, nthreads=THREADS)
+        assert c["w"] == c["m"] == c["v"] == 0, (k, c)
+        infos.append(gi)
+    opt.close()
+    return infos
+
+
+def test_config2_eko237m_full_size_bit_exact():
+    """272 tensors, 236,959,488 params, per-tensor sigma = 10^U(-5,-2),
+    loss scale 65536: two steps (fresh gradients), every element compared."""
+    specs = config_tensors("c2")
+    sig = H.log_uniform_sigmas(len(specs), 20260501)
+    infos = _full_size_steps("c2", sig, 65536.0, 2, 20260501)
+    assert all(i.applied for i in infos) and infos[-1].state.t == 2
+
+
+def test_config4_scaleup_full_size_bit_exact():
+    """218 tensors, 1,279,887,360 params, sigma 1e-3, loss scale 65536: one
+    step, every element compared."""
+    specs = config_tensors("c4")
+    infos = _full_size_steps("c4", [1e-3] * len(specs), 65536.0, 1, 7)
+    assert infos[0].applied == 1
+
+
+def test_config3_amp_stress_trajectory_5000_steps():
+    """EKO-237M, 5000 steps from scale 65536 (cap 2^24); on ~0.1 % of steps
+    (seeded) +inf, -inf or NaN at 1-16 seeded positions of random tensors.
+    Skip decisions, loss scale, t and counters must follow the oracle's
+    state machine at every step."""
+    import torch
+    specs = config_tensors("c3")
+    sig = H.log_uniform_sigmas(len(specs), 3)
+    ps = H.gpu_problem(specs, 3, HP["weight_decay"], sig, 65536.0)
+    cfg, opt = _opt(ps, 65536.0)
+    rng = np.random.default_rng(2026)
+    steps = 5000
+    bad_steps = np.nonzero(rng.random(steps) < 0.001)[0]
+    bad_steps = np.union1d(bad_steps, [1500, 1501, 2100])  # consecutive and mid-growth cases
+    specials = np.array([0x7C00, 0xFC00, 0x7E00], np.uint16).view(np.int16)
+    ref_state = _abi.State()
+    oracle.lib().ark_ref_state_init(opt.hp, ref_state)
+    g16 = [ps.g(i).view(torch.int16) for i in range(len(specs))]
+    events = np.zeros(steps, bool)
+    scales = []
+    for k in range(steps):
+        poked = []
+        if k in bad_steps:
+            events[k] = True
+            for _ in range(int(rng.integers(1, 17))):
+                ti = int(rng.integers(len(specs)))
+                pos = int(rng.integers(specs[ti].n))
+                poked.append((ti, pos, int(g16[ti][pos].item())))
+                g16[ti][pos] = int(specials[rng.integers(3)])
+        rc, gi = opt.step_all(cfg.lr, info=True)
+        rrc, _ = oracle.amp_replay(opt.hp, ref_state, events[k:k + 1])
+        assert rc == rrc and gi.applied == (not events[k]), k
+        assert gi.state.as_dict() == ref_state.as_dict(), (k, gi.state.as_dict())
+        for ti, pos, old in reversed(poked):
+            g16[ti][pos] = old
+        scales.append(gi.state.loss_scale)
+    # seeded schedule: skips at 1500, 1501, 2100 and 2717 halve 65536 down to
+    # 4096; 2000 clean steps later it doubles back to 8192
+    assert bad_steps.tolist() == [1500, 1501, 2100, 2717]
+    assert ref_state.t == steps - 4 and ref_state.skipped_steps == 4
+    assert min(scales) == 4096.0 and scales[-1] == 8192.0
+    assert scales.index(8192.0, 2717) == 2717 + 2000
+    opt.close()
+
+
+def test_state_set_get_and_restaurar_momentos():
+    """restaurar_momentos (optimizer.rs:237-313) on a small EKO set: moments
+    copied in checkpoint order, step set; wrong counts or sizes keep the
+    step, as the reference does."""
+    import torch
+    from ark_amd.eko import EkoConfig
+    specs = EkoConfig(n_layers=2, d_model=64, hidden=128, vocab=100).tensors()
+    ps = H.gpu_problem(specs, 1, 0.1, [1e-3] * len(specs), 1024.0)
+    cfg, opt = _opt(ps, 1024.0)
+    names = [s.name for s in specs]
+    layers = [i for i, s in enumerate(specs) if s.name not in ("embed", "gamma_final")]
+    order = [names.index("embed")] + layers + [names.index("gamma_final")]
+    rng = np.random.default_rng(0)
+    mm = [rng.random(specs[i].n).astype(np.float32) for i in order]
+    vv = [rng.random(specs[i].n).astype(np.float32) for i in order]
+    assert opt.restaurar_momentos(mm[:-2], vv[:-2], 77) is False       # wrong count
+    assert opt.step == 0
+    assert opt.restaurar_momentos(mm, vv, 1234) is True                # 1 + 9L + 1
+    assert opt.step == 1234
+    for k, i in enumerate(order):
+        assert np.array_equal(ps.m(i).cpu().numpy(), mm[k])
+        assert np.array_equal(ps.v(i).cpu().numpy(), vv[k])
+    assert opt.restaurar_momentos(mm[:-1], vv[:-1], 99) is True        # legacy 271-style
+    assert opt.step == 99
+    bad = list(mm)
+    bad[3] = bad[3][:-1]
+    assert opt.restaurar_momentos(bad, vv, 5) is False                 # layer size mismatch
+    assert opt.step == 99
+    opt.set_state(loss_scale=4096.0, clean_steps=1999)
+    _, info = opt.step_all(cfg.lr, info=True)
+    assert info.state.t == 100 and info.state.loss_scale == 8192.0 and info.state.clean_steps == 0
+    opt.close()
+
+
+def test_timing_counts_every_kernel():
+    specs = config_tensors("c1")
+    ps = H.gpu_problem(specs, 1, 0.1, [1e-3] * len(specs), 1024.0)
+    cfg, opt = _opt(ps, 1024.0)
+    opt.set_timing(True)
+    for _ in range(300):  # more than one event pool
+        opt.step_all(cfg.lr)
+    t = opt.get_timing()
+    assert t.steps == 300 and t.ms_adamw > 0 and t.ms_norm > 0 and t.ms_finalize > 0
+    assert t.ms_step >= t.ms_adamw
+    opt.set_timing(False)
+    opt.close()
+
+
+def test_many_handles_create_and_destroy():
+    specs = config_tensors("c0")
+    ps = H.gpu_problem(specs, 1, 0.1, [1e-3], 1024.0)
+    for _ in range(50):
+        cfg, opt = _opt(ps, 1024.0)
+        opt.step_all(cfg.lr)
+        opt.close()
+
+
+def test_create_rejects_short_or_host_buffers():
+    import torch
+    from ark_amd._lib import ArkOptError
+    from ark_amd.optimizer import AdamConfig, Optimizer, ParamSet
+    specs = config_tensors("c0")
+    ps = ParamSet(specs, 0.1)
+    tab = ps.table()
+    tab[0].n = 1 << 30  # 2 GiB of fp16: beyond the arena's allocation
+    with pytest.raises(ArkOptError, match="exceeds its allocation"):
+        Optimizer(AdamConfig(), ps, table=tab)
+    host = np.zeros(16, np.float32)
+    tab = ps.table()
+    tab[0].m = host.ctypes.data
+    with pytest.raises(ArkOptError, match="host memory|not memory known"):
+        Optimizer(AdamConfig(), ps, table=tab)
