@@ -159,11 +159,18 @@ def run_cpu_baseline(name, budget_s, threads):
 
 
 def traffic_from_profiles(name):
-    p = os.path.join(ROOT, "profiles", f"traffic_adamw_{name}.json")
+    """HBM-side bytes per adamw_kernel launch measured by rocprofv3 byte
+    counters (calibrated against a plain copy) for this workload, from the
+    committed profile summary; None when no profile of it is committed."""
+    p = os.path.join(ROOT, "profiles", f"adamw_kernel_{name}_traffic.txt")
     if not os.path.exists(p):
         return None, None
-    d = json.load(open(p))
-    return d.get("bytes_per_launch"), d.get("source")
+    kv = {}
+    for line in open(p):
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            kv[k.strip()] = v.strip()
+    return int(kv["bytes_per_launch"]), kv.get("source")
 
 
 def main():
