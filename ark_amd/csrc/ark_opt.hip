@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -123,8 +124,11 @@ struct ark_opt_handle {
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
-  double* d_part_sum = nullptr;  // kFinThreads * fin_leaves, zero past the partials
-  uint32_t fin_leaves = 1;
+  uint32_t* d_block_fast = nullptr;  // one flag per sumsq block
+  double* d_part_sum = nullptr;  // one partial per norm block, zero-padded
+  double* d_fold = nullptr;      // fold output when there are many partials
+  uint32_t padded_parts = 0;     // power of two >= parts when folding
+  uint32_t fin_leaves = 1;       // leaves per finalize thread
   ark_opt_state* d_state = nullptr;
   StepScalars* d_scal = nullptr;
   ark_opt_step_info* d_info = nullptr;
@@ -249,7 +253,14 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
     }
   }
   const uint64_t nseg = segs.size();
-  const int spb = ark::sumsq_spb(nseg);
+  int spb = ark::sumsq_spb(nseg);
+  // ARK_OPT_SUMSQ_SPB=8|16|32|64 overrides the segments per norm block (a
+  // tuning knob; the canonical tree makes the result independent of it).
+  if (const char* env = getenv("ARK_OPT_SUMSQ_SPB")) {
+    const int v = atoi(env);
+    if ((v == 8 || v == 16 || v == 32 || v == 64) && (nseg + v - 1) / v <= ark::kMaxParts)
+      spb = v;
+  }
   const uint64_t parts = (nseg + spb - 1) / spb;
   if (parts > ark::kMaxParts)
     return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
@@ -273,14 +284,35 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
 
-  // One allocation: segments | partial sums | flags | state | scalars | info
+  // One allocation: segments | block flags | partial sums | state | scalars | info
   size_t off = 0;
   const size_t o_seg = off;
   off = align_up(off + sizeof(SegDesc) * (size_t)(nseg ? nseg : 1), 256);
-  const uint32_t leaves = ark::finalize_leaves((uint32_t)parts);
-  const size_t psum_bytes = sizeof(double) * (size_t)ark::kFinThreads * leaves;
+  std::vector<uint32_t> block_fast((size_t)(parts ? parts : 1), 0u);
+  for (uint64_t b = 0; b < parts; ++b)
+    block_fast[(size_t)b] = ark::sumsq_block_fast(segs.data(), nseg, spb, b);
+  const size_t o_fast = off;
+  off = align_up(off + sizeof(uint32_t) * block_fast.size(), 256);
+  // Partials: up to kFinTarget go straight to the finalize (kFinThreads *
+  // leaves doubles, zero past the real ones); more are first folded in
+  // aligned groups of kFoldGroup from a power-of-two zero-padded buffer.
+  const bool fold = parts > ark::kFinTarget;
+  uint32_t padded = 0, leaves = 0;
+  size_t psum_bytes = 0, fold_bytes = 0;
+  if (fold) {
+    padded = ark::kFoldGroup;
+    while (padded < parts) padded <<= 1;
+    psum_bytes = sizeof(double) * (size_t)padded;
+    leaves = ark::finalize_leaves(padded / ark::kFoldGroup);
+    fold_bytes = sizeof(double) * (size_t)ark::kFinThreads * leaves;
+  } else {
+    leaves = ark::finalize_leaves((uint32_t)parts);
+    psum_bytes = sizeof(double) * (size_t)ark::kFinThreads * leaves;
+  }
   const size_t o_psum = off;
   off = align_up(off + psum_bytes, 256);
+  const size_t o_fold = off;
+  off = align_up(off + fold_bytes, 256);
   const size_t o_state = off;
   off = align_up(off + sizeof(ark_opt_state), 256);
   const size_t o_scal = off;
@@ -296,7 +328,10 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   }
   char* base = (char*)h->dev_mem;
   h->d_segs = (SegDesc*)(base + o_seg);
+  h->d_block_fast = (uint32_t*)(base + o_fast);
   h->d_part_sum = (double*)(base + o_psum);
+  h->d_fold = fold ? (double*)(base + o_fold) : nullptr;
+  h->padded_parts = padded;
   h->fin_leaves = leaves;
   h->d_state = (ark_opt_state*)(base + o_state);
   h->d_scal = (StepScalars*)(base + o_scal);
@@ -312,7 +347,11 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   StepScalars sc{};
   e = hipSuccess;
   if (nseg) e = hipMemcpy(h->d_segs, segs.data(), sizeof(SegDesc) * nseg, hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(h->d_block_fast, block_fast.data(), sizeof(uint32_t) * block_fast.size(),
+                  hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(h->d_part_sum, 0, psum_bytes);
+  if (e == hipSuccess && fold) e = hipMemset(h->d_fold, 0, fold_bytes);
   if (e == hipSuccess) e = hipMemcpy(h->d_state, &st, sizeof(st), hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(h->d_scal, &sc, sizeof(sc), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -355,11 +394,14 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
   }
   if (h->nseg) {
     ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
-                              h->nseg, h->d_state, h->d_part_sum, h->stream));
+                              h->nseg, h->d_block_fast, h->d_state, h->d_part_sum,
+                              h->stream));
+    if (h->d_fold)
+      ARK_HIP(ark::launch_fold(h->padded_parts, h->d_part_sum, h->d_fold, h->stream));
   }
   if (ev) ARK_HIP(hipEventRecord(ev[1], h->stream));
-  ARK_HIP(ark::launch_finalize(h->fin_leaves, h->d_part_sum, h->hp, lr, h->d_state,
-                               h->d_scal, h->d_info, h->stream));
+  ARK_HIP(ark::launch_finalize(h->fin_leaves, h->d_fold ? h->d_fold : h->d_part_sum, h->hp,
+                               lr, h->d_state, h->d_scal, h->d_info, h->stream));
   if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
   if (h->nseg) {
     ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->d_segs, h->nseg, h->d_scal,

@@ -167,93 +167,112 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // ---- kernel 1: sum of squares + non-finite flag -----------------------------
 
-// Block b covers segments [b*SPB, b*SPB + SPB) and writes the pairwise tree
-// of their 2*SPB half-segment sums: an aligned subtree of the global tree.
+// Block b covers segments [b*SPB, b*SPB + SPB) in batches of kRed = 8
+// segments.  Each batch reduces to the pairwise tree of its 16 half-segment
+// sums (an aligned subtree of the global tree); the block writes the pairwise
+// tree of its SPB/8 batch sums, again an aligned subtree.  Larger SPB keeps
+// the partial count, and so the finalize, small on big parameter sets.
 // A block that saw an inf or NaN gradient writes NaN, so the global sum is
 // NaN exactly when some gradient is non-finite (training.rs:291).
 template <typename GT, int SPB>
 __global__ __launch_bounds__(kBlock) void sumsq_kernel(
     const SegDesc* __restrict__ segs, uint32_t nseg,
-    const ark_opt_state* __restrict__ state, double* __restrict__ part_sum) {
-  constexpr int V = 2 * SPB;
-  static_assert(V <= 64, "one value index per lane of a wave");
+    const uint32_t* __restrict__ block_fast, const ark_opt_state* __restrict__ state,
+    double* __restrict__ part_sum) {
+  constexpr int kRed = 8;              // segments per in-block reduction
+  constexpr int NB = SPB / kRed;       // reductions per block
+  constexpr int V = 2 * kRed;          // half-segment values per lane
+  static_assert(SPB % kRed == 0 && (NB & (NB - 1)) == 0, "power-of-two batches");
   // segments whose loads are in flight together (register budget)
-  constexpr int kBatch = sizeof(GT) == 2 ? 8 : 4;
-  static_assert(SPB % kBatch == 0, "whole batches");
-  __shared__ double lds[kBlock / 64][V];
+  constexpr int kLoad = sizeof(GT) == 2 ? 8 : 4;
+  __shared__ double lds[2][kBlock / 64][V];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const float inv = 1.0f / state->loss_scale;  // training.rs:244
-  const uint32_t s0 = blockIdx.x * SPB;
+  // precomputed at create: all SPB segments exist, are full and 16-byte
+  // aligned (one scalar load instead of a chain of dependent checks)
+  const bool fast = block_fast[blockIdx.x] != 0u;
   uint32_t bad = 0;
-  double vals[V];
+  double bsum[NB];
 
-  bool fast = s0 + SPB <= nseg;
-  if (fast) {
 #pragma unroll
-    for (int k = 0; k < SPB; ++k)
-      fast = fast && segs[s0 + k].n == (uint32_t)kSeg && (segs[s0 + k].flags & kSegVec);
-  }
-  if (fast) {
-    // every lane issues all its loads of a batch before using any
+  for (int r = 0; r < NB; ++r) {
+    const uint32_t s0 = blockIdx.x * SPB + r * kRed;
+    double vals[V];
+    if (fast) {
+      // every lane issues all its loads of a batch before using any
 #pragma unroll
-    for (int b = 0; b < SPB; b += kBatch) {
-      typename GradIO<GT>::Raw8 raw[2 * kBatch];
-      float inv_k[kBatch];
+      for (int b = 0; b < kRed; b += kLoad) {
+        typename GradIO<GT>::Raw8 raw[2 * kLoad];
+        float inv_k[kLoad];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        const SegDesc& d = segs[s0 + b + k];
-        inv_k[k] = (d.flags & kSegNoUnscale) ? 1.0f : inv;
+        for (int k = 0; k < kLoad; ++k) {
+          const SegDesc& d = segs[s0 + b + k];
+          inv_k[k] = (d.flags & kSegNoUnscale) ? 1.0f : inv;
+          const GT* g = static_cast<const GT*>(d.g);
+          raw[2 * k] = GradIO<GT>::load8(g + tid * kVec);
+          raw[2 * k + 1] = GradIO<GT>::load8(g + kHalfSeg + tid * kVec);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * kLoad; ++i) {
+          float f[kVec];
+          GradIO<GT>::unpack8(raw[i], f, bad);
+          vals[2 * b + i] = group_sum(f, inv_k[i / 2]);
+        }
+      }
+    } else {
+      // ragged, unaligned or past-the-end segments: element by element
+#pragma unroll
+      for (int k = 0; k < kRed; ++k) {
+        const uint32_t s = s0 + k;
+        if (s >= nseg) {
+          vals[2 * k] = 0.0;
+          vals[2 * k + 1] = 0.0;
+          continue;
+        }
+        const SegDesc d = segs[s];
+        const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : inv;
         const GT* g = static_cast<const GT*>(d.g);
-        raw[2 * k] = GradIO<GT>::load8(g + tid * kVec);
-        raw[2 * k + 1] = GradIO<GT>::load8(g + kHalfSeg + tid * kVec);
-      }
 #pragma unroll
-      for (int i = 0; i < 2 * kBatch; ++i) {
-        float f[kVec];
-        GradIO<GT>::unpack8(raw[i], f, bad);
-        vals[2 * b + i] = group_sum(f, inv_k[i / 2]);
-      }
-    }
-  } else {
-    // ragged, unaligned or past-the-end segments: element by element
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t e0 = h * kHalfSeg + tid * kVec;
+          float f[kVec];
 #pragma unroll
-    for (int k = 0; k < SPB; ++k) {
-      const uint32_t s = s0 + k;
-      if (s >= nseg) {
-        vals[2 * k] = 0.0;
-        vals[2 * k + 1] = 0.0;
-        continue;
-      }
-      const SegDesc d = segs[s];
-      const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : inv;
-      const GT* g = static_cast<const GT*>(d.g);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t e0 = h * kHalfSeg + tid * kVec;
-        float f[kVec];
-#pragma unroll
-        for (int j = 0; j < kVec; ++j)
-          f[j] = (e0 + j < d.n) ? GradIO<GT>::load1(g + e0 + j, bad) : 0.0f;
-        vals[2 * k + h] = group_sum(f, inv_t);
+          for (int j = 0; j < kVec; ++j)
+            f[j] = (e0 + j < d.n) ? GradIO<GT>::load1(g + e0 + j, bad) : 0.0f;
+          vals[2 * k + h] = group_sum(f, inv_t);
+        }
       }
     }
-  }
 
-  int idx = 0;
-  transpose_reduce<V, 0>(vals, lane, idx);
-  const double wsum = butterfly_from<log2i(V)>(vals[0]);
-  if (lane < V) lds[wave][idx] = wsum;
-  const int any_bad = __syncthreads_or((int)bad);
-  if (wave == 0) {
+    int idx = 0;
+    transpose_reduce<V, 0>(vals, lane, idx);
+    const double wsum = butterfly_from<log2i(V)>(vals[0]);
+    // two LDS buffers: batch r+1 writes the other one while wave 0 reads
+    // this one; the barrier of batch r+1 orders the reuse of this one
+    if (lane < V) lds[r & 1][wave][idx] = wsum;
+    __syncthreads();
     double x = 0.0;
-    if (lane < V) x = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
-    // pairwise over the V half-segment sums in lane (= index) order
+    if (wave == 0) {
+      if (lane < V)
+        x = (lds[r & 1][0][lane] + lds[r & 1][1][lane]) +
+            (lds[r & 1][2][lane] + lds[r & 1][3][lane]);
+      // pairwise over the V half-segment sums in lane (= index) order
 #pragma unroll
-    for (int s = 0; s < log2i(V); ++s) x = x + __shfl_xor(x, 1 << s);
-    if (lane == 0) part_sum[blockIdx.x] = any_bad ? __builtin_nan("") : x;
+      for (int s = 0; s < log2i(V); ++s) x = x + __shfl_xor(x, 1 << s);
+    }
+    bsum[r] = x;
+  }
+  const int any_bad = __syncthreads_or((int)bad);
+  if (tid == 0) {
+    // pairwise over the batch sums in index order
+#pragma unroll
+    for (int w = NB / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int i = 0; i < w; ++i) bsum[i] = bsum[2 * i] + bsum[2 * i + 1];
+    part_sum[blockIdx.x] = any_bad ? __builtin_nan("") : bsum[0];
   }
 }
 
@@ -273,6 +292,16 @@ __device__ __forceinline__ double leaf_tree(const double* __restrict__ p) {
     const double b = leaf_tree<L / 2>(p + L / 2);
     return a + b;
   }
+}
+
+// Many partials: one wave per aligned group of kFoldGroup partials writes the
+// group's pairwise tree (again an aligned subtree), so the single-block
+// finalize never reads more than kFinTarget values.
+__global__ __launch_bounds__(kFoldGroup) void fold_kernel(const double* __restrict__ in,
+                                                          double* __restrict__ out) {
+  double x = in[blockIdx.x * kFoldGroup + threadIdx.x];
+  x = butterfly_from<0>(x);
+  if (threadIdx.x == 0) out[blockIdx.x] = x;
 }
 
 __device__ inline uint32_t amp_skip(const ark_opt_hparams& hp, ark_opt_state& st) {
@@ -491,22 +520,41 @@ __global__ __launch_bounds__(64) void adamw_single_kernel(
 
 }  // namespace
 
-int sumsq_spb(uint64_t nseg) { return (nseg + 7) / 8 <= kMaxParts ? 8 : 16; }
+int sumsq_spb(uint64_t nseg) {
+  // 8 segments per block measured fastest for the norm pass (16 and 32 cost
+  // 10-50 % more); larger blocks only when the partials would exceed
+  // kMaxParts (beyond 2^31 elements)
+  int spb = 8;
+  while (spb < 64 && (nseg + spb - 1) / spb > kMaxParts) spb *= 2;
+  return spb;
+}
+
+hipError_t launch_fold(uint32_t padded_parts, const double* in, double* out,
+                       hipStream_t stream) {
+  if (padded_parts % kFoldGroup) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fold_kernel, dim3(padded_parts / kFoldGroup), dim3(kFoldGroup), 0,
+                     stream, in, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
-                        const SegDesc* segs, uint32_t nseg,
+                        const SegDesc* segs, uint32_t nseg, const uint32_t* block_fast,
                         const ark_opt_state* state, double* part_sum,
                         hipStream_t stream) {
   const dim3 grid(nblocks), block(kBlock);
 #define ARK_SUMSQ(GT, SPB)                                                        \
   hipLaunchKernelGGL((sumsq_kernel<GT, SPB>), grid, block, 0, stream, segs, nseg, \
-                     state, part_sum)
-  if (grad_dtype == ARK_OPT_GRAD_F16) {
-    if (spb == 8) ARK_SUMSQ(uint16_t, 8);
-    else ARK_SUMSQ(uint16_t, 16);
-  } else {
-    if (spb == 8) ARK_SUMSQ(float, 8);
-    else ARK_SUMSQ(float, 16);
+                     block_fast, state, part_sum)
+  switch (spb * 2 + (grad_dtype == ARK_OPT_GRAD_F16 ? 0 : 1)) {
+    case 16: ARK_SUMSQ(uint16_t, 8); break;
+    case 32: ARK_SUMSQ(uint16_t, 16); break;
+    case 64: ARK_SUMSQ(uint16_t, 32); break;
+    case 128: ARK_SUMSQ(uint16_t, 64); break;
+    case 17: ARK_SUMSQ(float, 8); break;
+    case 33: ARK_SUMSQ(float, 16); break;
+    case 65: ARK_SUMSQ(float, 32); break;
+    case 129: ARK_SUMSQ(float, 64); break;
+    default: return hipErrorInvalidValue;
   }
 #undef ARK_SUMSQ
   return hipGetLastError();

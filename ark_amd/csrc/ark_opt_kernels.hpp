@@ -96,9 +96,18 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
-// Segments per sumsq block (8 or 16) and the resulting partial count.
+// Segments per sumsq block (8; 16, 32 or 64 only past kMaxParts partials).
 int sumsq_spb(uint64_t nseg);
-constexpr uint32_t kMaxParts = 64u * kFinThreads;  // finalize capacity
+constexpr uint32_t kMaxParts = 64u * kFinThreads;  // partial-buffer capacity
+// Above kFinTarget partials, fold_kernel first reduces aligned groups of
+// kFoldGroup (one wave each) so the finalize reads at most kFinTarget values.
+constexpr uint32_t kFinTarget = 8u * kFinThreads;
+constexpr uint32_t kFoldGroup = 64u;
+
+// in: padded_parts partials (a power of two, multiple of kFoldGroup, zero
+// past the real ones); out: padded_parts / kFoldGroup group sums.
+hipError_t launch_fold(uint32_t padded_parts, const double* in, double* out,
+                       hipStream_t stream);
 // adamw grid: one wave per row, 16 rows per segment; the grid must stay
 // below 2^32 work-items.
 constexpr uint64_t kMaxSegments = (1ull << 32) / (64ull * kRowsPerSeg) - 1;
@@ -108,11 +117,23 @@ constexpr uint64_t kMaxSegments = (1ull << 32) / (64ull * kRowsPerSeg) - 1;
 // ---------------------------------------------------------------------------
 
 // part_sum: one partial per block (NaN when the block saw a non-finite
-// gradient).
+// gradient).  block_fast[b] != 0 when block b's spb segments all exist, hold
+// kSeg elements and carry kSegVec (see sumsq_block_fast).
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
-                        const SegDesc* segs, uint32_t nseg,
+                        const SegDesc* segs, uint32_t nseg, const uint32_t* block_fast,
                         const ark_opt_state* state, double* part_sum,
                         hipStream_t stream);
+
+// Host-side computation of the block_fast flags for a descriptor list.
+inline uint32_t sumsq_block_fast(const SegDesc* segs, uint64_t nseg, int spb, uint64_t block) {
+  const uint64_t s0 = block * (uint64_t)spb;
+  if (s0 + (uint64_t)spb > nseg) return 0u;
+  for (int k = 0; k < spb; ++k) {
+    const SegDesc& d = segs[s0 + k];
+    if (d.n != (uint32_t)kSeg || !(d.flags & kSegVec)) return 0u;
+  }
+  return 1u;
+}
 
 // Leaves per finalize thread for nparts partials (a power of two <= 64); the
 // partial buffer must hold kFinThreads * leaves doubles, zero past nparts.
