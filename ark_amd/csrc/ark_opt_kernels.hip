@@ -187,19 +187,22 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
   constexpr int kLoad = sizeof(GT) == 2 ? 8 : 4;
   __shared__ double lds[2][kBlock / 64][V];
 
+  // Blocks run in reverse: the last block, which usually holds the ragged
+  // tail of the table, starts first instead of trailing the grid.
+  const uint32_t blk = gridDim.x - 1u - blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const float inv = 1.0f / state->loss_scale;  // training.rs:244
   // precomputed at create: all SPB segments exist, are full and 16-byte
   // aligned (one scalar load instead of a chain of dependent checks)
-  const bool fast = block_fast[blockIdx.x] != 0u;
+  const bool fast = block_fast[blk] != 0u;
   uint32_t bad = 0;
   double bsum[NB];
 
 #pragma unroll
   for (int r = 0; r < NB; ++r) {
-    const uint32_t s0 = blockIdx.x * SPB + r * kRed;
+    const uint32_t s0 = blk * SPB + r * kRed;
     double vals[V];
     if (fast) {
       // every lane issues all its loads of a batch before using any
@@ -223,7 +226,9 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
         }
       }
     } else {
-      // ragged, unaligned or past-the-end segments: element by element
+      // a block with some ragged, unaligned or past-the-end segment: full
+      // aligned segments still take the vector loads, the rest go element
+      // by element
 #pragma unroll
       for (int k = 0; k < kRed; ++k) {
         const uint32_t s = s0 + k;
@@ -235,6 +240,16 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
         const SegDesc d = segs[s];
         const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : inv;
         const GT* g = static_cast<const GT*>(d.g);
+        if (d.n == (uint32_t)kSeg && (d.flags & kSegVec)) {
+          const typename GradIO<GT>::Raw8 r0 = GradIO<GT>::load8(g + tid * kVec);
+          const typename GradIO<GT>::Raw8 r1 = GradIO<GT>::load8(g + kHalfSeg + tid * kVec);
+          float f[kVec];
+          GradIO<GT>::unpack8(r0, f, bad);
+          vals[2 * k] = group_sum(f, inv_t);
+          GradIO<GT>::unpack8(r1, f, bad);
+          vals[2 * k + 1] = group_sum(f, inv_t);
+          continue;
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t e0 = h * kHalfSeg + tid * kVec;
@@ -272,7 +287,7 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
     for (int w = NB / 2; w >= 1; w /= 2)
 #pragma unroll
       for (int i = 0; i < w; ++i) bsum[i] = bsum[2 * i] + bsum[2 * i + 1];
-    part_sum[blockIdx.x] = any_bad ? __builtin_nan("") : bsum[0];
+    part_sum[blk] = any_bad ? __builtin_nan("") : bsum[0];
   }
 }
 
