@@ -96,3 +96,12 @@ class Timing(C.Structure):
 
 
 STRUCTS = (Tensor, HParams, State, StepInfo, Timing)
+
+
+# include/ark_codec.h
+CODEC_F16_TO_F32 = 0
+CODEC_F32_TO_F16 = 1
+
+
+class CodecSpan(C.Structure):
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("n", C.c_uint64)]

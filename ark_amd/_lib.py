@@ -1,5 +1,5 @@
-"""Loader of the gfx950 library ark_amd/lib/libark_opt.so (C ABI of
-include/ark_opt.h and include/ark_synth.h).
+"""Loader of the gfx950 library ark_amd/lib/libark_opt.so (the C ABI declared
+in include/*.h).
 
 There is no fallback: if the library is missing or fails to load, every
 caller gets an ImportError-like failure with the reason.
@@ -46,6 +46,12 @@ def _declare(L):
         "ark_synth_normal_f32": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_fill_u16": ([P, u64, C.c_uint16, P], C.c_int),
         "ark_synth_copy": ([P, P, u64, P], C.c_int),
+        "ark_hip_dequant_f16_to_f32": ([P, P, u64, P], C.c_int),
+        "ark_hip_quant_f32_to_f16": ([P, P, u64, P], C.c_int),
+        "ark_codec_plan_create": ([C.POINTER(_abi.CodecSpan), i32, u32, P, C.POINTER(H)],
+                                  C.c_int),
+        "ark_codec_plan_run": ([H], C.c_int),
+        "ark_codec_plan_destroy": ([H], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -1,0 +1,46 @@
+// ark_common.hpp -- host-side helpers shared by every C-ABI entry point of
+// libark_opt.so: the thread-local last-error message, HIP error mapping,
+// device guard and the caller-buffer check.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ark_opt.h"
+
+namespace ark {
+
+// Records a printf-style message as the calling thread's last error (read
+// back with ark_opt_last_error) and returns code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// fail(ARK_OPT_EHIP, "<what>: <hip error string> (<code>)").
+int hip_fail(hipError_t e, const char* what);
+
+// The message behind ark_opt_last_error().
+const char* last_error();
+
+// Host-side bounds check of a caller buffer: it must be device-accessible
+// memory and [p, p + bytes) must lie inside its allocation when the runtime
+// can tell the allocation range.  Catches host pointers and short buffers
+// before any kernel touches them.  what/idx name the buffer in the message.
+int check_buffer(const void* p, uint64_t bytes, const char* what, int idx);
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev);
+  ~DeviceGuard();
+};
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace ark
+
+#define ARK_HIP(call)                                       \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return ark::hip_fail(e_, #call);  \
+  } while (0)

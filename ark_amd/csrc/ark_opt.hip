@@ -3,7 +3,6 @@
 // the per-step launch sequence, state get/set, timing, and the single-tensor
 // drop-in of ark_asm_adam_step_f16.
 #include <math.h>
-#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -11,86 +10,19 @@
 #include <string>
 #include <vector>
 
+#include "ark_common.hpp"
 #include "ark_opt_kernels.hpp"
 
 using ark::SegDesc;
 using ark::StepScalars;
 
+using ark::align_up;
+using ark::check_buffer;
+using ark::DeviceGuard;
+using ark::fail;
+using ark::hip_fail;
+
 namespace {
-
-thread_local std::string g_last_error;
-
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-int fail(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return code;
-}
-
-int hip_fail(hipError_t e, const char* what) {
-  return fail(ARK_OPT_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
-}
-
-#define ARK_HIP(call)                                   \
-  do {                                                  \
-    hipError_t e_ = (call);                             \
-    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
-  } while (0)
-
-// Restores the caller's current device on scope exit.
-struct DeviceGuard {
-  int prev = -1;
-  bool ok = false;
-  explicit DeviceGuard(int dev) {
-    if (hipGetDevice(&prev) != hipSuccess) return;
-    ok = (prev == dev) || (hipSetDevice(dev) == hipSuccess);
-  }
-  ~DeviceGuard() {
-    int cur = -1;
-    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-  }
-};
-
-// Host-side bounds check of a caller buffer: it must be device-accessible
-// memory and [p, p + bytes) must lie inside its allocation when the runtime
-// can tell the allocation range.  Catches host pointers and short buffers
-// before any kernel touches them.
-int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
-  if (bytes == 0) return ARK_OPT_OK;
-  if (p == nullptr) return fail(ARK_OPT_EINVAL, "tensor %d: %s is NULL", idx, what);
-  hipPointerAttribute_t attr;
-  hipError_t e = hipPointerGetAttributes(&attr, p);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is not memory known to HIP", idx,
-                what, p);
-  }
-  const bool device_ok = attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged ||
-                         attr.type == hipMemoryTypeArray || attr.type == hipMemoryTypeUnified ||
-                         (attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr);
-  if (!device_ok) {
-    return fail(ARK_OPT_EINVAL, "tensor %d: %s (%p) is host memory the device cannot access",
-                idx, what, p);
-  }
-  hipDeviceptr_t base = nullptr;
-  size_t size = 0;
-  e = hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p);
-  if (e == hipSuccess && base != nullptr) {
-    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
-    if (q < b || q - b > size || bytes > size - (q - b)) {
-      return fail(ARK_OPT_EINVAL,
-                  "tensor %d: %s [%p, +%llu B) exceeds its allocation [%p, +%zu B)",
-                  idx, what, p, (unsigned long long)bytes, base, size);
-    }
-  } else {
-    (void)hipGetLastError();
-  }
-  return ARK_OPT_OK;
-}
 
 bool finite_f(float x) { return isfinite(x) != 0; }
 
@@ -172,15 +104,13 @@ void free_handle(ark_opt_handle* h) {
   delete h;
 }
 
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
 }  // namespace
 
 extern "C" {
 
 int ark_opt_abi_version(void) { return ARK_OPT_ABI_VERSION; }
 
-const char* ark_opt_last_error(void) { return g_last_error.c_str(); }
+const char* ark_opt_last_error(void) { return ark::last_error(); }
 
 int ark_opt_struct_sizes(size_t* out, int n) {
   const size_t s[5] = {sizeof(ark_opt_tensor), sizeof(ark_opt_hparams),

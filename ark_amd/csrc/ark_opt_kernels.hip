@@ -15,43 +15,13 @@
 // cache-allocating loads, which leaves up to the Infinity Cache's 256 MB of
 // them resident for the AdamW pass that re-reads them right after (~5 %
 // faster AdamW on EKO-237M, within one step, so real training sees it too).
+#include "ark_device.hpp"
 #include "ark_opt_kernels.hpp"
 
 namespace ark {
 namespace {
 
-#define ARK_GLOBAL __attribute__((address_space(1)))
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-__device__ __forceinline__ T ld_nt(const void* p) {
-  return __builtin_nontemporal_load((const ARK_GLOBAL T*)p);
-}
-template <typename T>
-__device__ __forceinline__ void st_nt(void* p, T v) {
-  __builtin_nontemporal_store(v, (ARK_GLOBAL T*)p);
-}
-template <typename T>
-__device__ __forceinline__ T ld_g(const void* p) {
-  return *(const ARK_GLOBAL T*)p;
-}
-template <typename T>
-__device__ __forceinline__ void st_g(void* p, T v) {
-  *(ARK_GLOBAL T*)p = v;
-}
-
-__device__ __forceinline__ float h2f(uint32_t b) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
-}
-// The empty asm makes f opaque, so the preceding fp32 arithmetic can never be
-// merged with the conversion into a single-rounding mixed-precision fma: the
-// reference rounds to fp32 (fsub) and then to fp16 (fcvtn).
-__device__ __forceinline__ uint32_t f2h(float f) {
-  asm("" : "+v"(f));
-  return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
+using namespace dev;
 
 // ---- gradient access --------------------------------------------------------
 

@@ -173,6 +173,75 @@ def traffic_from_profiles(name):
     return int(kv["bytes_per_launch"]), kv.get("source")
 
 
+def run_codec(a):
+    """The weight codec over EKO-237M (include/ark_codec.h): one launch
+    dequantising all 272 fp16 weight tensors to fp32 (the per-step loop of
+    training.rs:162-186), and one quantising them back (sync_weights_to_gpu,
+    memory.rs:347-377).  6 B per element each way."""
+    import torch
+    from ark_amd import codec
+    from ark_amd.eko import config_tensors
+    torch.cuda.set_device(0)
+    specs = config_tensors("c2")
+    n = sum(s.n for s in specs)
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+    w16 = [(torch.randn(s.n, device="cuda", generator=g) * 0.02).half() for s in specs]
+    f32 = [torch.empty(s.n, dtype=torch.float32, device="cuda") for s in specs]
+    back = [torch.empty(s.n, dtype=torch.float16, device="cuda") for s in specs]
+    dq = codec.CodecPlan(list(zip(w16, f32)), "f16_to_f32")
+    qt = codec.CodecPlan(list(zip(f32, back)), "f32_to_f16")
+    res = {}
+    for name, plan in (("dequant", dq), ("quant", qt)):
+        for _ in range(a.warmup):
+            plan.run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(a.steps):
+            plan.run()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / a.steps
+        res[name] = dict(ms=e0.elapsed_time(e1) / a.steps, wall_ms=wall)
+    ok = all(torch.equal(x.view(torch.int16), y.view(torch.int16)) for x, y in zip(w16, back))
+    dq.close(), qt.close()
+    cpu = None
+    if not a.no_cpu:
+        import numpy as np
+        import oracle
+        from concurrent.futures import ThreadPoolExecutor
+        th = a.cpu_threads or min(16, os.cpu_count() or 1)
+        src = w16[0].view(torch.int16).cpu().numpy().view(np.uint16)  # the 24.6M-element embed
+        parts = np.array_split(src, th)
+        reps, t0 = 0, time.perf_counter()
+        with ThreadPoolExecutor(th) as ex:
+            while time.perf_counter() - t0 < min(a.cpu_seconds, 10.0):
+                list(ex.map(oracle.f16_to_f32, parts))
+                reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(6 * src.size * reps / el / 1e9, 3), unit="GB/s", cores=th,
+                   kind="port", sample=f"{reps} dequantisations of the {src.size}-element "
+                   f"embedding in {el:.1f} s on {th} threads")
+    d = res["dequant"]
+    gbs = 6 * n / (d["ms"] * 1e-3) / 1e9
+    q_gbs = 6 * n / (res["quant"]["ms"] * 1e-3) / 1e9
+    out = {
+        "metric": "EKO-237M weight dequant fp16->fp32, all tensors, GB/s (1 GPU)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(d["ms"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "codec: 272 EKO-237M weight tensors, one launch per direction",
+                   "elements": n, "bytes_per_launch": 6 * n, "round_trip_exact": bool(ok),
+                   "quant_ms": round(res["quant"]["ms"], 4), "quant_GBs": round(q_gbs, 2)},
+        "roofline": {"kernel": "codec_batch<f16_to_f32>", "bound": "hbm", "achieved": round(gbs, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": 6 * n},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +251,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--path", default="step", choices=["step", "codec"],
+                    help="step: the optimizer step (headline); codec: the weight codec")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -189,6 +260,9 @@ def main():
         print("bench.py measures one GPU only: the optimizer step of this build runs on a "
               "single MI355X (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if a.path == "codec":
+        run_codec(a)
+        return
 
     r = run_gpu(a.workload, a.steps, a.warmup)
     if a.calib_copy:

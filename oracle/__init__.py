@@ -51,6 +51,9 @@ def lib():
     L.ark_ref_check_f16_to_f32_f16c.restype = C.c_int64
     L.ark_ref_check_f32_to_f16_f16c.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
     L.ark_ref_check_f32_to_f16_f16c.restype = C.c_int64
+    L.ark_ref_compare_f32_to_f16_range.argtypes = [C.c_uint64, C.c_uint64, P, C.c_int,
+                                                   C.POINTER(C.c_uint64)]
+    L.ark_ref_compare_f32_to_f16_range.restype = C.c_int64
     L.ark_ref_pow_binary.argtypes = [C.c_float, C.c_uint32]
     L.ark_ref_pow_binary.restype = C.c_float
     L.ark_ref_prologue.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float,
@@ -109,6 +112,16 @@ def f32_to_f16(x):
     out = np.empty(x.shape, np.uint16)
     lib().ark_ref_f32_to_f16_array(_ptr(x), _ptr(out), x.size)
     return out
+
+
+def compare_f32_to_f16_range(lo, got, nthreads=8):
+    """Mismatches of got (uint16, one per fp32 pattern lo, lo+1, ...) against
+    the conversion of those patterns, and the first mismatching pattern."""
+    got = np.ascontiguousarray(got, dtype=np.uint16)
+    first = C.c_uint64()
+    bad = lib().ark_ref_compare_f32_to_f16_range(lo, lo + got.size, _ptr(got), nthreads,
+                                                 C.byref(first))
+    return bad, (None if first.value == 2 ** 64 - 1 else first.value)
 
 
 def pow_binary(beta, t):

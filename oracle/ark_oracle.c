@@ -144,8 +144,6 @@ static void split_range(uint64_t n, int tid, int nth, uint64_t *lo,
 /* Exhaustive checks against F16C hardware conversion.                       */
 /* ------------------------------------------------------------------------ */
 
-static int f32_is_nan(uint32_t u) { return (u & 0x7FFFFFFFu) > 0x7F800000u; }
-static int f16_is_nan(uint16_t h) { return (h & 0x7FFFu) > 0x7C00u; }
 
 int64_t ark_ref_check_f16_to_f32_f16c(void) {
 #if defined(__F16C__)
@@ -153,11 +151,7 @@ int64_t ark_ref_check_f16_to_f32_f16c(void) {
   for (uint32_t h = 0; h < 65536u; ++h) {
     uint32_t a = f2u(ark_ref_f16_to_f32((uint16_t)h));
     uint32_t b = f2u(_cvtsh_ss((unsigned short)h));
-    if (f32_is_nan(a) || f32_is_nan(b)) {
-      bad += (f32_is_nan(a) != f32_is_nan(b));
-    } else {
-      bad += (a != b);
-    }
+    bad += (a != b); /* NaNs too: F16C quiets and keeps the payload like fcvtl */
   }
   return bad;
 #else
@@ -182,11 +176,7 @@ static void chk32_worker(void *p, int tid, int nth) {
     float f = u2f((uint32_t)i);
     uint16_t a = ark_ref_f32_to_f16(f);
     uint16_t b = (uint16_t)_cvtss_sh(f, 0); /* imm 0: round to nearest even */
-    if (f16_is_nan(a) || f16_is_nan(b)) {
-      bad += (f16_is_nan(a) != f16_is_nan(b));
-    } else {
-      bad += (a != b);
-    }
+    bad += (a != b); /* NaNs too: F16C truncates the payload and quiets like fcvtn */
   }
   c->bad[tid] = bad;
 #else
@@ -214,6 +204,54 @@ int64_t ark_ref_check_f32_to_f16_f16c(uint64_t lo, uint64_t hi, int nthreads) {
   (void)nthreads;
   return -1;
 #endif
+}
+
+/* Compares got[i] with the conversion of the bit pattern lo + i, for the
+ * patterns [lo, hi); returns the number of mismatches and the first one. */
+typedef struct {
+  uint64_t lo, hi;
+  const uint16_t *got;
+  int64_t *bad;
+  uint64_t *first;
+} cmp32_ctx;
+
+static void cmp32_worker(void *p, int tid, int nth) {
+  cmp32_ctx *c = (cmp32_ctx *)p;
+  uint64_t lo, hi;
+  split_range(c->hi - c->lo, tid, nth, &lo, &hi);
+  int64_t bad = 0;
+  uint64_t first = UINT64_MAX;
+  for (uint64_t i = lo; i < hi; ++i) {
+    uint16_t want = ark_ref_f32_to_f16(u2f((uint32_t)(c->lo + i)));
+    if (want != c->got[i]) {
+      if (first == UINT64_MAX) first = c->lo + i;
+      ++bad;
+    }
+  }
+  c->bad[tid] = bad;
+  c->first[tid] = first;
+}
+
+int64_t ark_ref_compare_f32_to_f16_range(uint64_t lo, uint64_t hi, const uint16_t *got,
+                                         int nthreads, uint64_t *first_bad) {
+  if (nthreads < 1) nthreads = 1;
+  if (hi > (1ull << 32)) hi = 1ull << 32;
+  if (first_bad) *first_bad = UINT64_MAX;
+  if (lo >= hi) return 0;
+  int64_t *bad = (int64_t *)calloc((size_t)nthreads, sizeof(int64_t));
+  uint64_t *first = (uint64_t *)calloc((size_t)nthreads, sizeof(uint64_t));
+  cmp32_ctx c = {lo, hi, got, bad, first};
+  run_parallel(nthreads, cmp32_worker, &c);
+  int64_t tot = 0;
+  uint64_t f = UINT64_MAX;
+  for (int i = 0; i < nthreads; ++i) {
+    tot += bad[i];
+    if (first[i] < f) f = first[i];
+  }
+  free(bad);
+  free(first);
+  if (first_bad) *first_bad = f;
+  return tot;
 }
 
 /* ------------------------------------------------------------------------ */

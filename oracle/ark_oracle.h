@@ -32,10 +32,18 @@ void ark_ref_f32_to_f16_array(const float *in, uint16_t *out, uint64_t n);
 
 /* Exhaustive cross-checks of the software conversions against the x86 F16C
  * hardware conversion (vcvtph2ps / vcvtps2ph in RNE).  Return the number of
- * mismatching inputs (NaNs compare as a class), or -1 without F16C.
+ * mismatching bit patterns (NaN payloads included: F16C follows the same
+ * quiet-and-keep-payload rule as fcvtl / fcvtn), or -1 without F16C.
  * f32->f16 covers the inputs [lo, hi) of the 2^32 bit patterns. */
 int64_t ark_ref_check_f16_to_f32_f16c(void);
 int64_t ark_ref_check_f32_to_f16_f16c(uint64_t lo, uint64_t hi, int nthreads);
+
+/* got[i] against ark_ref_f32_to_f16 of the bit pattern lo + i for the patterns
+ * [lo, hi): the number of mismatches; *first_bad = the first mismatching
+ * pattern (UINT64_MAX if none).  Used to check a device conversion of every
+ * fp32 pattern. */
+int64_t ark_ref_compare_f32_to_f16_range(uint64_t lo, uint64_t hi, const uint16_t *got,
+                                         int nthreads, uint64_t *first_bad);
 
 /* beta^t by the binary exponentiation of opti.s:223-235 (t used as given). */
 float ark_ref_pow_binary(float beta, uint32_t t);
