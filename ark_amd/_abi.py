@@ -12,6 +12,7 @@ EARLY_STOP = 1
 EINVAL = -1
 EHIP = -2
 ENOMEM = -3
+EIO = -4
 
 NORM_SEGMENT = 4096
 
@@ -105,3 +106,24 @@ CODEC_F32_TO_F16 = 1
 
 class CodecSpan(C.Structure):
     _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("n", C.c_uint64)]
+
+
+# include/ark_ckpt.h
+CKPT_F16 = 0
+CKPT_F32 = 1
+CKPT_MAGIC_V2 = 0x4B325241
+CKPT_MAGIC_V3 = 0x4B335241
+CKPT_MAGIC_V4 = 0x4B345241
+CKPT_MAGIC_AMP = 0x53504D41
+
+
+class CkptRecord(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("n", C.c_uint64), ("dtype", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class CkptInfo(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("has_moments", C.c_uint32),
+                ("global_step", C.c_uint64), ("adam_step", C.c_uint64),
+                ("n_tensors", C.c_uint64), ("file_bytes", C.c_uint64),
+                ("has_amp", C.c_uint32), ("reserved", C.c_uint32)]

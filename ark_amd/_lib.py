@@ -52,6 +52,18 @@ def _declare(L):
                                   C.c_int),
         "ark_codec_plan_run": ([H], C.c_int),
         "ark_codec_plan_destroy": ([H], C.c_int),
+        "ark_ckpt_save_v4": ([C.c_char_p, u64, u64, C.POINTER(_abi.CkptRecord), i32,
+                              C.POINTER(_abi.State), P], C.c_int),
+        "ark_ckpt_probe": ([C.c_char_p, C.POINTER(_abi.CkptInfo), C.POINTER(u64),
+                            C.POINTER(u32), i32], C.c_int),
+        "ark_ckpt_load": ([C.c_char_p, C.POINTER(_abi.CkptRecord), i32,
+                           C.POINTER(_abi.CkptInfo), C.POINTER(_abi.State), P], C.c_int),
+        "ark_ckpt_v4_image_bytes": ([C.POINTER(_abi.CkptRecord), i32, C.c_int, C.POINTER(u64)],
+                                    C.c_int),
+        "ark_ckpt_v4_pack": ([C.POINTER(_abi.CkptRecord), i32, u64, u64, C.POINTER(_abi.State),
+                              P, u64, P], C.c_int),
+        "ark_ckpt_v4_unpack": ([P, u64, C.POINTER(_abi.CkptRecord), i32, C.POINTER(u32), P],
+                               C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

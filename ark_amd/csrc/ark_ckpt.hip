@@ -1,0 +1,857 @@
+// ark_ckpt.hip -- ARK checkpoint files from and to device buffers
+// (include/ark_ckpt.h).
+//
+// The V4 format has no alignment: a 28-byte file header, then per tensor a
+// 16-byte header and the raw data, so after the first tensor every data
+// block starts at an arbitrary byte offset.  The kernels work in 16-byte
+// chunks of the aligned side and shift the other side into place:
+//
+//   pack_kernel   one block per <= 16 KiB of image inside one tensor's data
+//                 (the block finds its tensor in a per-tensor table);
+//                 a lane owns aligned 16-byte image chunks, loads the two
+//                 aligned 16-byte source blocks that cover the chunk and
+//                 funnel-shifts them (v_alignbyte_b32) by the tensor's
+//                 uniform misalignment.  Chunks that straddle a tensor's
+//                 edge, or whose second block would pass the end of the
+//                 source, go byte by byte.
+//   header_kernel the file header, tensor headers and trailer, byte stores.
+//   unpack_kernel one block per 4096 elements of one tensor (found the same
+//                 way, both file types in one launch); a lane takes
+//                 16-byte units of the image (8 fp16 or 4 fp32 elements),
+//                 shifts them out of two aligned loads, converts to the
+//                 destination type and stores aligned.
+//
+// All HBM bound: 2 bytes of traffic per image byte (one read, one write).
+// Files move through two pinned staging buffers, copy and file I/O
+// overlapped.
+#include <errno.h>
+#include <fcntl.h>
+#include <string.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <vector>
+
+#include "ark_ckpt.h"
+#include "ark_common.hpp"
+#include "ark_device.hpp"
+
+namespace {
+
+using namespace ark::dev;
+using ark::fail;
+
+constexpr uint64_t kFileHeaderV4 = 28;  // u32 magic + 3 x u64 (io.rs:453-456)
+constexpr uint64_t kRecHeaderV4 = 16;   // u64 n + u64 type (io.rs:460-461, :467-468)
+constexpr uint64_t kTrailerBytes = 40;  // u32 magic + u32 version + ark_opt_state
+constexpr uint32_t kTrailerVersion = 1;
+constexpr int kThreads = 256;
+constexpr uint32_t kPackSegBytes = 16384;             // image bytes per pack block
+constexpr int kPackChunks = kPackSegBytes / (16 * kThreads);  // 4 per lane
+constexpr uint32_t kUnpackSeg = 4096;                 // elements per unpack block
+constexpr size_t kStageBytes = (size_t)64 << 20;      // per pinned staging buffer
+static_assert(sizeof(ark_opt_state) == 32, "trailer holds a 32-byte state");
+
+inline uint64_t esize(uint32_t t) { return t == ARK_CKPT_F16 ? 2u : 4u; }
+
+struct HdrPiece {  // up to 16 header bytes at an image offset
+  uint64_t off;
+  uint32_t len;
+  uint32_t pad;
+  uint8_t bytes[16];
+};
+static_assert(sizeof(HdrPiece) == 32, "32-byte piece");
+
+// Per-tensor tables: block b of a launch belongs to the tensor r with
+// start[r] <= b < start[r + 1] (start[] holds n_tensors + 1 prefix counts;
+// a binary search over it, scalar loads that stay in the scalar cache).
+struct PackRec {
+  const uint8_t* src;  // the tensor's first data byte (device)
+  uint64_t data_off;   // image offset of that byte
+  uint64_t src_bytes;  // the tensor's data bytes
+  uint32_t src_vec;    // src 16-byte aligned
+  uint32_t pad;
+};
+static_assert(sizeof(PackRec) == 32, "32-byte descriptor");
+
+struct UnpackRec {
+  void* dst;         // the tensor's first destination element
+  uint64_t src_off;  // image offset of its first element
+  uint64_t n;        // elements
+  uint8_t dtype;     // destination element type
+  uint8_t ftype;     // file element type
+  uint8_t dst_vec;   // dst 16-byte aligned
+  uint8_t pad[5];
+};
+static_assert(sizeof(UnpackRec) == 32, "32-byte descriptor");
+
+struct CheckDesc {  // expected tensor header at an image offset
+  uint64_t hdr_off;
+  uint64_t n;
+  uint32_t type;
+  uint32_t pad;
+};
+
+// ---- device side ------------------------------------------------------------
+
+// Bytes [sh, sh + 16) of the 32 bytes a|b (little endian); sh in 0..15 and
+// uniform across the wave, so the word selection is a scalar branch.
+__device__ __forceinline__ u32x4 funnel16(const u32x4 a, const u32x4 b, uint32_t sh) {
+  const uint32_t sb = sh & 3u;
+  uint32_t w0, w1, w2, w3, w4;
+  switch (sh >> 2) {
+    case 0: w0 = a.x; w1 = a.y; w2 = a.z; w3 = a.w; w4 = b.x; break;
+    case 1: w0 = a.y; w1 = a.z; w2 = a.w; w3 = b.x; w4 = b.y; break;
+    case 2: w0 = a.z; w1 = a.w; w2 = b.x; w3 = b.y; w4 = b.z; break;
+    default: w0 = a.w; w1 = b.x; w2 = b.y; w3 = b.z; w4 = b.w; break;
+  }
+  u32x4 r;
+  r.x = __builtin_amdgcn_alignbyte(w1, w0, sb);
+  r.y = __builtin_amdgcn_alignbyte(w2, w1, sb);
+  r.z = __builtin_amdgcn_alignbyte(w3, w2, sb);
+  r.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return ld_g<uint8_t>(p); }
+__device__ __forceinline__ void st_u8(uint8_t* p, uint32_t v) { st_g<uint8_t>(p, (uint8_t)v); }
+
+__global__ __launch_bounds__(kThreads) void header_kernel(const HdrPiece* __restrict__ pieces,
+                                                          uint32_t npieces,
+                                                          uint8_t* __restrict__ img) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= npieces) return;
+  const HdrPiece p = pieces[i];
+  for (uint32_t b = 0; b < p.len; ++b) st_u8(img + p.off + b, p.bytes[b]);
+}
+
+// The tensor that block b belongs to (see PackRec).
+__device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start, uint32_t nrec,
+                                             uint32_t b) {
+  uint32_t lo = 0, hi = nrec;  // start[lo] <= b < start[hi]
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (start[mid] <= b)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// Block j of a tensor covers image bytes [base + j*S, base + (j+1)*S) of its
+// data, base = data_off rounded down to 16, clipped to the data.
+__global__ __launch_bounds__(kThreads) void pack_kernel(const PackRec* __restrict__ recs,
+                                                        const uint32_t* __restrict__ start,
+                                                        uint32_t nrec, uint8_t* __restrict__ img) {
+  const uint32_t r = find_rec(start, nrec, blockIdx.x);
+  const PackRec s = recs[r];
+  const uint64_t base = s.data_off & ~15ull;
+  const uint64_t end = s.data_off + s.src_bytes;
+  const uint64_t c0 = base + (uint64_t)(blockIdx.x - start[r]) * kPackSegBytes;
+  const uint64_t seg_lo = c0 > s.data_off ? c0 : s.data_off;
+  const uint64_t seg_hi = c0 + kPackSegBytes < end ? c0 + kPackSegBytes : end;
+#pragma unroll
+  for (int k = 0; k < kPackChunks; ++k) {
+    const uint64_t c = c0 + 16ull * (uint64_t)(k * kThreads + threadIdx.x);
+    if (c >= seg_hi) break;
+    const uint64_t lo = c > seg_lo ? c : seg_lo;
+    const uint64_t hi = c + 16 < seg_hi ? c + 16 : seg_hi;
+    if (lo == c && hi == c + 16 && s.src_vec) {
+      const uint64_t so = c - s.data_off;
+      const uint64_t a0 = so & ~15ull;
+      const uint32_t sh = (uint32_t)(so & 15u);
+      if (sh == 0) {
+        st_nt<u32x4>(img + c, ld_nt<u32x4>(s.src + a0));
+        continue;
+      }
+      if (a0 + 32 <= s.src_bytes) {
+        const u32x4 a = ld_nt<u32x4>(s.src + a0);
+        const u32x4 b = ld_nt<u32x4>(s.src + a0 + 16);
+        st_nt<u32x4>(img + c, funnel16(a, b, sh));
+        continue;
+      }
+    }
+    for (uint64_t b = lo; b < hi; ++b) st_u8(img + b, ld_u8(s.src + (b - s.data_off)));
+  }
+}
+
+// fp16 -> fp16 through fp32 (half's to_f32, then fcvtn): every value kept,
+// a signalling NaN comes back quiet.
+__device__ __forceinline__ uint32_t quiet16(uint32_t h) {
+  return ((h & 0x7C00u) == 0x7C00u && (h & 0x03FFu) != 0u) ? (h | 0x0200u) : h;
+}
+__device__ __forceinline__ uint32_t quiet16x2(uint32_t w) {
+  return quiet16(w & 0xFFFFu) | (quiet16(w >> 16) << 16);
+}
+
+// One 16-byte unit of the image in file type FT, converted to dtype and
+// stored at dst (aligned for the destination width).
+template <uint32_t FT>
+__device__ __forceinline__ void store_unit(const u32x4 v, uint32_t dtype, uint8_t* dst) {
+  if constexpr (FT == ARK_CKPT_F16) {  // 8 elements
+    if (dtype == ARK_CKPT_F16) {
+      u32x4 r;
+      r.x = quiet16x2(v.x); r.y = quiet16x2(v.y); r.z = quiet16x2(v.z); r.w = quiet16x2(v.w);
+      st_nt<u32x4>(dst, r);
+    } else {
+      u32x4 a, b;
+      a.x = f16_to_f32_bits(v.x & 0xFFFFu); a.y = f16_to_f32_bits(v.x >> 16);
+      a.z = f16_to_f32_bits(v.y & 0xFFFFu); a.w = f16_to_f32_bits(v.y >> 16);
+      b.x = f16_to_f32_bits(v.z & 0xFFFFu); b.y = f16_to_f32_bits(v.z >> 16);
+      b.z = f16_to_f32_bits(v.w & 0xFFFFu); b.w = f16_to_f32_bits(v.w >> 16);
+      st_nt<u32x4>(dst, a);
+      st_nt<u32x4>(dst + 16, b);
+    }
+  } else {  // 4 elements
+    if (dtype == ARK_CKPT_F32) {
+      st_nt<u32x4>(dst, v);
+    } else {
+      u32x2 h;
+      h.x = f32_to_f16_bits(v.x) | (f32_to_f16_bits(v.y) << 16);
+      h.y = f32_to_f16_bits(v.z) | (f32_to_f16_bits(v.w) << 16);
+      st_nt<u32x2>(dst, h);
+    }
+  }
+}
+
+template <uint32_t FT>
+__device__ __forceinline__ void unpack_elem(const uint8_t* src, uint32_t dtype, uint8_t* dst) {
+  if constexpr (FT == ARK_CKPT_F16) {
+    const uint32_t h = ld_u8(src) | (ld_u8(src + 1) << 8);
+    if (dtype == ARK_CKPT_F16)
+      st_g<uint16_t>(dst, (uint16_t)quiet16(h));
+    else
+      st_g<uint32_t>(dst, f16_to_f32_bits(h));
+  } else {
+    const uint32_t x = ld_u8(src) | (ld_u8(src + 1) << 8) | (ld_u8(src + 2) << 16) |
+                       (ld_u8(src + 3) << 24);
+    if (dtype == ARK_CKPT_F32)
+      st_g<uint32_t>(dst, x);
+    else
+      st_g<uint16_t>(dst, (uint16_t)f32_to_f16_bits(x));
+  }
+}
+
+template <uint32_t FT>
+__device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begin,
+                                             const uint8_t* __restrict__ img, uint64_t img_bytes) {
+  constexpr uint32_t kFs = FT == ARK_CKPT_F16 ? 2u : 4u;  // file element bytes
+  constexpr uint32_t kU = 16u / kFs;                       // elements per unit
+  constexpr int kUnits = (int)(kUnpackSeg / kU / kThreads);  // 2 or 4 per lane
+  const uint32_t ds = s.dtype == ARK_CKPT_F16 ? 2u : 4u;
+  const uint64_t src_off = s.src_off + e_begin * kFs;
+  const uint32_t sh = (uint32_t)(src_off & 15u);
+  const uint64_t n = s.n - e_begin < kUnpackSeg ? s.n - e_begin : kUnpackSeg;
+  uint8_t* dst0 = (uint8_t*)s.dst + e_begin * ds;
+#pragma unroll
+  for (int k = 0; k < kUnits; ++k) {
+    const uint32_t e0 = ((uint32_t)k * kThreads + threadIdx.x) * kU;
+    if (e0 >= n) break;
+    const uint64_t sb = src_off + (uint64_t)e0 * kFs;
+    const uint64_t a0 = sb & ~15ull;
+    uint8_t* dst = dst0 + (uint64_t)e0 * ds;
+    if (s.dst_vec && e0 + kU <= n) {
+      if (sh == 0) {
+        store_unit<FT>(ld_nt<u32x4>(img + a0), s.dtype, dst);
+        continue;
+      }
+      if (a0 + 32 <= img_bytes) {
+        const u32x4 a = ld_nt<u32x4>(img + a0);
+        const u32x4 b = ld_nt<u32x4>(img + a0 + 16);
+        store_unit<FT>(funnel16(a, b, sh), s.dtype, dst);
+        continue;
+      }
+    }
+    for (uint32_t j = 0; j < kU && e0 + j < n; ++j)
+      unpack_elem<FT>(img + sb + (uint64_t)j * kFs, s.dtype, dst + (uint64_t)j * ds);
+  }
+}
+
+// Block j of a tensor converts its elements [j*4096, (j+1)*4096).
+__global__ __launch_bounds__(kThreads) void unpack_kernel(const UnpackRec* __restrict__ recs,
+                                                          const uint32_t* __restrict__ start,
+                                                          uint32_t nrec,
+                                                          const uint8_t* __restrict__ img,
+                                                          uint64_t img_bytes) {
+  const uint32_t r = find_rec(start, nrec, blockIdx.x);
+  const UnpackRec s = recs[r];
+  const uint64_t e_begin = (uint64_t)(blockIdx.x - start[r]) * kUnpackSeg;
+  if (s.ftype == ARK_CKPT_F16)
+    unpack_block<ARK_CKPT_F16>(s, e_begin, img, img_bytes);
+  else
+    unpack_block<ARK_CKPT_F32>(s, e_begin, img, img_bytes);
+}
+
+__device__ __forceinline__ uint64_t ld_u64_bytes(const uint8_t* p) {
+  uint64_t x = 0;
+  for (int i = 0; i < 8; ++i) x |= (uint64_t)ld_u8(p + i) << (8 * i);
+  return x;
+}
+
+// Thread i < n checks tensor header i; thread n checks the file header.  The
+// smallest failing index (n for the file header) lands in *bad.
+__global__ __launch_bounds__(kThreads) void check_kernel(const CheckDesc* __restrict__ d,
+                                                         uint32_t n, const uint8_t* __restrict__ img,
+                                                         uint32_t* __restrict__ bad) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  if (i > n) return;
+  bool ok;
+  if (i == n) {
+    const uint32_t magic = (uint32_t)ld_u8(img) | (ld_u8(img + 1) << 8) | (ld_u8(img + 2) << 16) |
+                           (ld_u8(img + 3) << 24);
+    ok = magic == ARK_CKPT_MAGIC_V4 && ld_u64_bytes(img + 20) == (uint64_t)n;
+  } else {
+    const CheckDesc c = d[i];
+    const uint64_t fn = ld_u64_bytes(img + c.hdr_off);
+    const uint64_t ft = ld_u64_bytes(img + c.hdr_off + 8);
+    // io.rs:534: type 0 is F16, anything else is read as F32
+    ok = fn == c.n && ((ft == 0) == (c.type == ARK_CKPT_F16));
+  }
+  if (!ok) atomicMin(bad, i);
+}
+
+// ---- host side --------------------------------------------------------------
+
+struct DevBuf {
+  void* p = nullptr;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+};
+// Stream-ordered allocation from the device's default memory pool (no
+// device-wide synchronisation on free), for the small descriptor tables.
+struct StreamBuf {
+  void* p = nullptr;
+  hipStream_t s = nullptr;
+  hipError_t alloc(size_t bytes, hipStream_t stream) {
+    s = stream;
+    return hipMallocAsync(&p, bytes, stream);
+  }
+  ~StreamBuf() {
+    if (p) (void)hipFreeAsync(p, s);
+  }
+};
+struct PinBuf {
+  void* p = nullptr;
+  ~PinBuf() {
+    if (p) (void)hipHostFree(p);
+  }
+};
+// Waits for the stream on scope exit: declared after the buffers a queued
+// copy or kernel may still use, so it runs before they are freed.
+struct StreamSync {
+  hipStream_t s;
+  ~StreamSync() { (void)hipStreamSynchronize(s); }
+};
+struct Fd {
+  int fd = -1;
+  ~Fd() {
+    if (fd >= 0) ::close(fd);
+  }
+};
+
+struct Layout {
+  std::vector<uint64_t> hdr, data;
+  uint64_t end = 0;    // first byte after the last tensor
+  uint64_t total = 0;  // end + trailer
+};
+
+int check_records(const ark_ckpt_record* r, int32_t n, bool need_device) {
+  if (n < 0 || (n > 0 && !r)) return fail(ARK_OPT_EINVAL, "record table is NULL or n < 0");
+  ark::BufferChecker checker;
+  for (int32_t i = 0; i < n; ++i) {
+    if (r[i].dtype != ARK_CKPT_F16 && r[i].dtype != ARK_CKPT_F32)
+      return fail(ARK_OPT_EINVAL, "record %d: dtype %u unknown", i, r[i].dtype);
+    if (r[i].n > (1ull << 48)) return fail(ARK_OPT_EINVAL, "record %d: n too large", i);
+    if (((uintptr_t)r[i].data) % esize(r[i].dtype))
+      return fail(ARK_OPT_EINVAL, "record %d: data not aligned to its element", i);
+    if (need_device) {
+      int rc = checker.check(r[i].data, r[i].n * esize(r[i].dtype), "data", i);
+      if (rc) return rc;
+    }
+  }
+  return ARK_OPT_OK;
+}
+
+Layout v4_layout(const ark_ckpt_record* r, int32_t n, const uint32_t* types, bool amp) {
+  Layout L;
+  L.hdr.resize((size_t)n);
+  L.data.resize((size_t)n);
+  uint64_t off = kFileHeaderV4;
+  for (int32_t i = 0; i < n; ++i) {
+    L.hdr[i] = off;
+    off += kRecHeaderV4;
+    L.data[i] = off;
+    off += r[i].n * esize(types ? types[i] : r[i].dtype);
+  }
+  L.end = off;
+  L.total = off + (amp ? kTrailerBytes : 0);
+  return L;
+}
+
+void put_bytes(std::vector<HdrPiece>& v, uint64_t off, const uint8_t* b, uint32_t len) {
+  for (uint32_t k = 0; k < len; k += 16) {
+    HdrPiece p{};
+    p.off = off + k;
+    p.len = len - k < 16 ? len - k : 16;
+    memcpy(p.bytes, b + k, p.len);
+    v.push_back(p);
+  }
+}
+
+template <typename T>
+void le(uint8_t* dst, T v) {  // little endian, as the hosts this runs on
+  memcpy(dst, &v, sizeof(T));
+}
+
+// Header pieces and data descriptors of a V4 image, uploaded, then both
+// kernels queued on stream and waited for.
+int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
+               const ark_opt_state* amp, uint8_t* img, hipStream_t stream) {
+  const Layout L = v4_layout(r, n, nullptr, amp != nullptr);
+  std::vector<HdrPiece> pieces;
+  uint8_t fh[kFileHeaderV4];
+  le<uint32_t>(fh, ARK_CKPT_MAGIC_V4);
+  le<uint64_t>(fh + 4, gs);
+  le<uint64_t>(fh + 12, as);
+  le<uint64_t>(fh + 20, (uint64_t)n);
+  put_bytes(pieces, 0, fh, kFileHeaderV4);
+  std::vector<PackRec> recs((size_t)n);
+  std::vector<uint32_t> start((size_t)n + 1);
+  uint64_t blocks = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    uint8_t rh[kRecHeaderV4];
+    le<uint64_t>(rh, r[i].n);
+    le<uint64_t>(rh + 8, (uint64_t)r[i].dtype);
+    put_bytes(pieces, L.hdr[i], rh, kRecHeaderV4);
+    const uint64_t bytes = r[i].n * esize(r[i].dtype);
+    PackRec& pr = recs[i];
+    pr = PackRec{};
+    pr.src = (const uint8_t*)r[i].data;
+    pr.data_off = L.data[i];
+    pr.src_bytes = bytes;
+    pr.src_vec = ((uintptr_t)r[i].data & 15u) == 0;
+    start[i] = (uint32_t)blocks;
+    if (bytes) {
+      const uint64_t base = L.data[i] & ~15ull;
+      blocks += (L.data[i] + bytes - base + kPackSegBytes - 1) / kPackSegBytes;
+    }
+    if (blocks > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "image too large");
+  }
+  start[n] = (uint32_t)blocks;
+  if (amp) {
+    uint8_t tr[kTrailerBytes];
+    le<uint32_t>(tr, ARK_CKPT_MAGIC_AMP);
+    le<uint32_t>(tr + 4, kTrailerVersion);
+    memcpy(tr + 8, amp, sizeof(ark_opt_state));
+    put_bytes(pieces, L.end, tr, kTrailerBytes);
+  }
+  // one upload: header pieces | tensor table | block starts
+  const size_t pb = pieces.size() * sizeof(HdrPiece), rb = recs.size() * sizeof(PackRec);
+  const size_t stb = start.size() * sizeof(uint32_t);
+  std::vector<uint8_t> host(pb + rb + stb);
+  memcpy(host.data(), pieces.data(), pb);
+  if (rb) memcpy(host.data() + pb, recs.data(), rb);
+  memcpy(host.data() + pb + rb, start.data(), stb);
+  StreamBuf d;
+  hipError_t e = d.alloc(host.size(), stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for checkpoint descriptors failed",
+                host.size());
+  }
+  StreamSync sync{stream};
+  HdrPiece* dp = (HdrPiece*)d.p;
+  const PackRec* dr = (const PackRec*)((char*)d.p + pb);
+  const uint32_t* dst = (const uint32_t*)((char*)d.p + pb + rb);
+  ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
+  const uint32_t np = (uint32_t)pieces.size();
+  hipLaunchKernelGGL(header_kernel, dim3((np + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                     stream, dp, np, img);
+  ARK_HIP(hipGetLastError());
+  if (blocks) {
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, dr, dst,
+                       (uint32_t)n, img);
+    ARK_HIP(hipGetLastError());
+  }
+  ARK_HIP(hipStreamSynchronize(stream));
+  return ARK_OPT_OK;
+}
+
+// Unpack descriptors of every record, grouped by file type, launched and
+// waited for.
+int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* r, int32_t n,
+                 const std::vector<uint64_t>& data_off, const std::vector<uint32_t>& ftype,
+                 hipStream_t stream) {
+  std::vector<UnpackRec> recs((size_t)n);
+  std::vector<uint32_t> start((size_t)n + 1);
+  uint64_t blocks = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    UnpackRec& u = recs[i];
+    u = UnpackRec{};
+    u.dst = r[i].data;
+    u.src_off = data_off[i];
+    u.n = r[i].n;
+    u.dtype = (uint8_t)r[i].dtype;
+    u.ftype = (uint8_t)ftype[i];
+    u.dst_vec = ((uintptr_t)r[i].data & 15u) == 0;
+    start[i] = (uint32_t)blocks;
+    blocks += (r[i].n + kUnpackSeg - 1) / kUnpackSeg;
+    if (blocks > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "checkpoint too large");
+  }
+  start[n] = (uint32_t)blocks;
+  if (blocks == 0) return ARK_OPT_OK;
+  const size_t rb = recs.size() * sizeof(UnpackRec), stb = start.size() * sizeof(uint32_t);
+  std::vector<uint8_t> host(rb + stb);
+  memcpy(host.data(), recs.data(), rb);
+  memcpy(host.data() + rb, start.data(), stb);
+  StreamBuf d;
+  hipError_t e = d.alloc(host.size(), stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for checkpoint descriptors failed",
+                host.size());
+  }
+  StreamSync sync{stream};
+  ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
+  hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
+                     (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb), (uint32_t)n, img,
+                     img_bytes);
+  ARK_HIP(hipGetLastError());
+  ARK_HIP(hipStreamSynchronize(stream));
+  return ARK_OPT_OK;
+}
+
+int io_fail(const char* what, const char* path) {
+  return fail(ARK_OPT_EIO, "%s %s: %s", what, path, strerror(errno));
+}
+
+int read_exact(int fd, void* buf, uint64_t len, uint64_t off, const char* path) {
+  uint8_t* p = (uint8_t*)buf;
+  while (len) {
+    const ssize_t k = pread(fd, p, len > (1u << 30) ? (1u << 30) : len, (off_t)off);
+    if (k < 0) {
+      if (errno == EINTR) continue;
+      return io_fail("read", path);
+    }
+    if (k == 0) return fail(ARK_OPT_EIO, "%s: unexpected end of file at byte %llu", path,
+                            (unsigned long long)off);
+    p += k;
+    off += (uint64_t)k;
+    len -= (uint64_t)k;
+  }
+  return ARK_OPT_OK;
+}
+
+int write_all(int fd, const void* buf, uint64_t len, const char* path) {
+  const uint8_t* p = (const uint8_t*)buf;
+  while (len) {
+    const ssize_t k = ::write(fd, p, len > (1u << 30) ? (1u << 30) : len);
+    if (k < 0) {
+      if (errno == EINTR) continue;
+      return io_fail("write", path);
+    }
+    p += k;
+    len -= (uint64_t)k;
+  }
+  return ARK_OPT_OK;
+}
+
+// Header walk of a checkpoint file (io.rs:504-671): version, steps, and per
+// tensor its n, file type and data offset; checks that every tensor lies
+// inside the file (the reference's read_exact fails there) and looks for the
+// AMP trailer after the last one.
+struct Parsed {
+  ark_ckpt_info info{};
+  std::vector<uint64_t> n, data;
+  std::vector<uint32_t> type;
+  uint64_t end = 0;
+  ark_opt_state amp{};
+};
+
+int parse_file(int fd, const char* path, Parsed* P) {
+  struct stat st;
+  if (fstat(fd, &st) != 0) return io_fail("stat", path);
+  const uint64_t size = (uint64_t)st.st_size;
+  uint8_t h[28];
+  int rc;
+  if (size < 12) return fail(ARK_OPT_EIO, "%s: %llu bytes, too short for a checkpoint", path,
+                             (unsigned long long)size);
+  if ((rc = read_exact(fd, h, 12, 0, path))) return rc;
+  uint32_t magic;
+  memcpy(&magic, h, 4);
+  ark_ckpt_info& I = P->info;
+  memset(&I, 0, sizeof(I));
+  I.file_bytes = size;
+  uint64_t off;
+  memcpy(&I.global_step, h + 4, 8);
+  if (magic == ARK_CKPT_MAGIC_V4 || magic == ARK_CKPT_MAGIC_V3) {
+    if ((rc = read_exact(fd, h, 16, 12, path))) return rc;
+    memcpy(&I.adam_step, h, 8);
+    memcpy(&I.n_tensors, h + 8, 8);
+    I.version = magic == ARK_CKPT_MAGIC_V4 ? 4 : 3;
+    I.has_moments = 1;
+    off = 28;
+  } else if (magic == ARK_CKPT_MAGIC_V2) {
+    if ((rc = read_exact(fd, h, 8, 12, path))) return rc;
+    memcpy(&I.n_tensors, h, 8);
+    I.version = 2;
+    off = 20;
+  } else {
+    return fail(ARK_OPT_EIO, "%s: bad magic 0x%08X (not an ARK checkpoint)", path, magic);
+  }
+  const uint64_t hb = I.version == 4 ? 16 : 8;
+  if (I.n_tensors > (size - off) / hb)
+    return fail(ARK_OPT_EIO, "%s: %llu tensors cannot fit in %llu bytes", path,
+                (unsigned long long)I.n_tensors, (unsigned long long)size);
+  P->n.resize(I.n_tensors);
+  P->data.resize(I.n_tensors);
+  P->type.resize(I.n_tensors);
+  for (uint64_t i = 0; i < I.n_tensors; ++i) {
+    if (off + hb > size)
+      return fail(ARK_OPT_EIO, "%s: truncated at tensor %llu header", path, (unsigned long long)i);
+    if ((rc = read_exact(fd, h, hb, off, path))) return rc;
+    uint64_t n, t = 1;
+    memcpy(&n, h, 8);
+    if (hb == 16) memcpy(&t, h + 8, 8);
+    const uint32_t ft = t == 0 ? ARK_CKPT_F16 : ARK_CKPT_F32;  // io.rs:534
+    off += hb;
+    const uint64_t bytes = n * esize(ft);
+    if (n > (1ull << 48) || bytes > size - off)
+      return fail(ARK_OPT_EIO, "%s: truncated in tensor %llu (n=%llu)", path,
+                  (unsigned long long)i, (unsigned long long)n);
+    P->n[i] = n;
+    P->type[i] = ft;
+    P->data[i] = off;
+    off += bytes;
+  }
+  P->end = off;
+  if (I.version == 4 && size - off >= kTrailerBytes) {
+    uint8_t tr[kTrailerBytes];
+    if ((rc = read_exact(fd, tr, kTrailerBytes, off, path))) return rc;
+    uint32_t m, v;
+    memcpy(&m, tr, 4);
+    memcpy(&v, tr + 4, 4);
+    if (m == ARK_CKPT_MAGIC_AMP && v == kTrailerVersion) {
+      I.has_amp = 1;
+      memcpy(&P->amp, tr + 8, sizeof(ark_opt_state));
+    }
+  }
+  return ARK_OPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ark_ckpt_v4_image_bytes(const ark_ckpt_record* records, int32_t n, int with_amp,
+                            uint64_t* bytes) {
+  if (!bytes) return fail(ARK_OPT_EINVAL, "bytes is NULL");
+  int rc = check_records(records, n, false);
+  if (rc) return rc;
+  *bytes = v4_layout(records, n, nullptr, with_amp != 0).total;
+  return ARK_OPT_OK;
+}
+
+int ark_ckpt_v4_pack(const ark_ckpt_record* records, int32_t n, uint64_t global_step,
+                     uint64_t adam_step, const ark_opt_state* amp, void* image,
+                     uint64_t image_bytes, void* stream) {
+  int rc = check_records(records, n, true);
+  if (rc) return rc;
+  const Layout L = v4_layout(records, n, nullptr, amp != nullptr);
+  if (image_bytes < L.total)
+    return fail(ARK_OPT_EINVAL, "image holds %llu bytes, the checkpoint needs %llu",
+                (unsigned long long)image_bytes, (unsigned long long)L.total);
+  if ((uintptr_t)image & 15u) return fail(ARK_OPT_EINVAL, "image not 16-byte aligned");
+  if ((rc = ark::check_buffer(image, L.total, "image", 0))) return rc;
+  return pack_image(records, n, global_step, adam_step, amp, (uint8_t*)image,
+                    (hipStream_t)stream);
+}
+
+int ark_ckpt_v4_unpack(const void* image, uint64_t image_bytes, const ark_ckpt_record* records,
+                       int32_t n, const uint32_t* file_types, void* stream) {
+  int rc = check_records(records, n, true);
+  if (rc) return rc;
+  if (n > 0 && !file_types) return fail(ARK_OPT_EINVAL, "file_types is NULL");
+  for (int32_t i = 0; i < n; ++i)
+    if (file_types[i] != ARK_CKPT_F16 && file_types[i] != ARK_CKPT_F32)
+      return fail(ARK_OPT_EINVAL, "file_types[%d] = %u unknown", i, file_types[i]);
+  const Layout L = v4_layout(records, n, file_types, false);
+  if (image_bytes < L.end)
+    return fail(ARK_OPT_EINVAL, "image holds %llu bytes, the layout needs %llu",
+                (unsigned long long)image_bytes, (unsigned long long)L.end);
+  if ((uintptr_t)image & 15u) return fail(ARK_OPT_EINVAL, "image not 16-byte aligned");
+  if ((rc = ark::check_buffer(image, image_bytes, "image", 0))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // header check on the device
+  std::vector<CheckDesc> cd((size_t)n);
+  for (int32_t i = 0; i < n; ++i) cd[i] = CheckDesc{L.hdr[i], records[i].n, file_types[i], 0};
+  DevBuf d;
+  const size_t cb = cd.size() * sizeof(CheckDesc);
+  hipError_t e = hipMalloc(&d.p, cb + 16);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMalloc(%zu) failed", cb + 16);
+  }
+  StreamSync sync{s};
+  uint32_t* dbad = (uint32_t*)((char*)d.p + cb);
+  const uint32_t init = 0xFFFFFFFFu;
+  if (cb) ARK_HIP(hipMemcpyAsync(d.p, cd.data(), cb, hipMemcpyHostToDevice, s));
+  ARK_HIP(hipMemcpyAsync(dbad, &init, 4, hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(check_kernel, dim3((uint32_t)(n + 1 + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, s, (const CheckDesc*)d.p, (uint32_t)n,
+                     (const uint8_t*)image, dbad);
+  ARK_HIP(hipGetLastError());
+  uint32_t bad = 0;
+  ARK_HIP(hipMemcpyAsync(&bad, dbad, 4, hipMemcpyDeviceToHost, s));
+  ARK_HIP(hipStreamSynchronize(s));
+  if (bad == (uint32_t)n)
+    return fail(ARK_OPT_EIO, "image: V4 file header missing or n_tensors != %d", n);
+  if (bad != 0xFFFFFFFFu)
+    return fail(ARK_OPT_EIO, "image: tensor %u header does not match the record (n=%llu)", bad,
+                (unsigned long long)records[bad].n);
+  std::vector<uint32_t> ft(file_types, file_types + n);
+  return unpack_image((const uint8_t*)image, image_bytes, records, n, L.data, ft, s);
+}
+
+int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
+                     const ark_ckpt_record* records, int32_t n, const ark_opt_state* amp,
+                     void* stream) {
+  if (!path) return fail(ARK_OPT_EINVAL, "path is NULL");
+  int rc = check_records(records, n, true);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const Layout L = v4_layout(records, n, nullptr, amp != nullptr);
+  DevBuf img;
+  hipError_t e = hipMalloc(&img.p, L.total + 16);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMalloc(%llu) for the checkpoint image failed",
+                (unsigned long long)L.total);
+  }
+  if ((rc = pack_image(records, n, global_step, adam_step, amp, (uint8_t*)img.p, s))) return rc;
+  const size_t stage = L.total < kStageBytes ? (size_t)L.total : kStageBytes;
+  PinBuf pin[2];
+  for (auto& p : pin) {
+    if ((e = hipHostMalloc(&p.p, stage, hipHostMallocDefault)) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(ARK_OPT_ENOMEM, "hipHostMalloc(%zu) failed", stage);
+    }
+  }
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  for (auto& x : ev) ARK_HIP(hipEventCreateWithFlags(&x, hipEventDisableTiming));
+  struct EvGuard {
+    hipEvent_t* e;
+    ~EvGuard() {
+      for (int i = 0; i < 2; ++i)
+        if (e[i]) (void)hipEventDestroy(e[i]);
+    }
+  } eg{ev};
+  StreamSync sync{s};
+  Fd f;
+  f.fd = ::open(path, O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+  if (f.fd < 0) return io_fail("create", path);
+  // chunk k: D2H into pin[k & 1]; while it runs, write chunk k - 1
+  const uint64_t nchunks = (L.total + stage - 1) / stage;
+  for (uint64_t k = 0; k <= nchunks; ++k) {
+    if (k < nchunks) {
+      const uint64_t off = k * stage;
+      const uint64_t len = L.total - off < stage ? L.total - off : stage;
+      ARK_HIP(hipMemcpyAsync(pin[k & 1].p, (char*)img.p + off, len, hipMemcpyDeviceToHost, s));
+      ARK_HIP(hipEventRecord(ev[k & 1], s));
+    }
+    if (k > 0) {
+      const uint64_t j = k - 1;
+      const uint64_t off = j * stage;
+      const uint64_t len = L.total - off < stage ? L.total - off : stage;
+      ARK_HIP(hipEventSynchronize(ev[j & 1]));
+      if ((rc = write_all(f.fd, pin[j & 1].p, len, path))) return rc;
+    }
+  }
+  const int fd = f.fd;
+  f.fd = -1;
+  if (::close(fd) != 0) return io_fail("close", path);
+  return ARK_OPT_OK;
+}
+
+int ark_ckpt_probe(const char* path, ark_ckpt_info* info, uint64_t* n_out, uint32_t* type_out,
+                   int32_t max) {
+  if (!path) return fail(ARK_OPT_EINVAL, "path is NULL");
+  Fd f;
+  f.fd = ::open(path, O_RDONLY | O_CLOEXEC);
+  if (f.fd < 0) return io_fail("open", path);
+  Parsed P;
+  int rc = parse_file(f.fd, path, &P);
+  if (rc) return rc;
+  if (info) *info = P.info;
+  for (int32_t i = 0; i < max && (uint64_t)i < P.info.n_tensors; ++i) {
+    if (n_out) n_out[i] = P.n[i];
+    if (type_out) type_out[i] = P.type[i];
+  }
+  return ARK_OPT_OK;
+}
+
+int ark_ckpt_load(const char* path, const ark_ckpt_record* records, int32_t n,
+                  ark_ckpt_info* info, ark_opt_state* amp, void* stream) {
+  if (!path) return fail(ARK_OPT_EINVAL, "path is NULL");
+  int rc = check_records(records, n, true);
+  if (rc) return rc;
+  Fd f;
+  f.fd = ::open(path, O_RDONLY | O_CLOEXEC);
+  if (f.fd < 0) return io_fail("open", path);
+  Parsed P;
+  if ((rc = parse_file(f.fd, path, &P))) return rc;
+  if (P.info.n_tensors != (uint64_t)n)
+    return fail(ARK_OPT_EINVAL, "%s holds %llu tensors, %d records given", path,
+                (unsigned long long)P.info.n_tensors, n);
+  for (int32_t i = 0; i < n; ++i)
+    if (P.n[i] != records[i].n)
+      return fail(ARK_OPT_EINVAL, "%s: tensor %d has n=%llu, record %d has n=%llu", path, i,
+                  (unsigned long long)P.n[i], i, (unsigned long long)records[i].n);
+  hipStream_t s = (hipStream_t)stream;
+  const uint64_t total = P.end;
+  DevBuf img;
+  hipError_t e = hipMalloc(&img.p, total + 16);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMalloc(%llu) for the checkpoint image failed",
+                (unsigned long long)total);
+  }
+  const size_t stage = total < kStageBytes ? (size_t)total : kStageBytes;
+  PinBuf pin[2];
+  for (auto& p : pin) {
+    if ((e = hipHostMalloc(&p.p, stage ? stage : 16, hipHostMallocDefault)) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(ARK_OPT_ENOMEM, "hipHostMalloc(%zu) failed", stage);
+    }
+  }
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  for (auto& x : ev) ARK_HIP(hipEventCreateWithFlags(&x, hipEventDisableTiming));
+  struct EvGuard {
+    hipEvent_t* e;
+    ~EvGuard() {
+      for (int i = 0; i < 2; ++i)
+        if (e[i]) (void)hipEventDestroy(e[i]);
+    }
+  } eg{ev};
+  StreamSync sync{s};
+  // chunk k: read into pin[k & 1] once its previous copy (chunk k - 2) is
+  // done, then H2D on the stream
+  const uint64_t nchunks = stage ? (total + stage - 1) / stage : 0;
+  for (uint64_t k = 0; k < nchunks; ++k) {
+    const uint64_t off = k * stage;
+    const uint64_t len = total - off < stage ? total - off : stage;
+    if (k >= 2) ARK_HIP(hipEventSynchronize(ev[k & 1]));
+    if ((rc = read_exact(f.fd, pin[k & 1].p, len, off, path))) return rc;
+    ARK_HIP(hipMemcpyAsync((char*)img.p + off, pin[k & 1].p, len, hipMemcpyHostToDevice, s));
+    ARK_HIP(hipEventRecord(ev[k & 1], s));
+  }
+  if ((rc = unpack_image((const uint8_t*)img.p, total, records, n, P.data, P.type, s)))
+    return rc;
+  if (info) *info = P.info;
+  if (amp && P.info.has_amp) *amp = P.amp;
+  return ARK_OPT_OK;
+}
+
+}  // extern "C"

@@ -173,6 +173,7 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
   const uint64_t ss = direction == ARK_CODEC_F16_TO_F32 ? 2u : 4u;
   const uint64_t ds = direction == ARK_CODEC_F16_TO_F32 ? 4u : 2u;
   std::vector<CodecSeg> segs;
+  ark::BufferChecker checker;
   int rc;
   for (int32_t i = 0; i < n_spans; ++i) {
     const ark_codec_span& s = spans[i];
@@ -180,8 +181,8 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
     if (((uintptr_t)s.src % ss) || ((uintptr_t)s.dst % ds))
       return ark::fail(ARK_OPT_EINVAL, "span %d: src or dst not aligned to its element", i);
     if (s.n > (1ull << 48)) return ark::fail(ARK_OPT_EINVAL, "span %d: n too large", i);
-    if ((rc = ark::check_buffer(s.src, s.n * ss, "src", i))) return rc;
-    if ((rc = ark::check_buffer(s.dst, s.n * ds, "dst", i))) return rc;
+    if ((rc = checker.check(s.src, s.n * ss, "src", i))) return rc;
+    if ((rc = checker.check(s.dst, s.n * ds, "dst", i))) return rc;
     if (overlaps(s.src, s.n * ss, s.dst, s.n * ds))
       return ark::fail(ARK_OPT_EINVAL, "span %d: src and dst overlap", i);
     const uint32_t vec = ((((uintptr_t)s.src | (uintptr_t)s.dst) & 15u) == 0) ? 1u : 0u;

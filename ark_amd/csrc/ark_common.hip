@@ -28,7 +28,14 @@ int hip_fail(hipError_t e, const char* what) {
 
 const char* last_error() { return g_last_error.c_str(); }
 
-int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
+namespace {
+
+// check_buffer, also returning the allocation range when the runtime knows it
+// (*size = 0 when it does not).
+int check_buffer_range(const void* p, uint64_t bytes, const char* what, int idx,
+                       uintptr_t* rbase, size_t* rsize) {
+  *rbase = 0;
+  *rsize = 0;
   if (bytes == 0) return ARK_OPT_OK;
   if (p == nullptr) return fail(ARK_OPT_EINVAL, "buffer %d: %s is NULL", idx, what);
   hipPointerAttribute_t attr;
@@ -55,10 +62,39 @@ int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
                   "buffer %d: %s [%p, +%llu B) exceeds its allocation [%p, +%zu B)",
                   idx, what, p, (unsigned long long)bytes, base, size);
     }
+    *rbase = b;
+    *rsize = size;
   } else {
     (void)hipGetLastError();
   }
   return ARK_OPT_OK;
+}
+
+}  // namespace
+
+int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
+  uintptr_t b;
+  size_t s;
+  return check_buffer_range(p, bytes, what, idx, &b, &s);
+}
+
+int BufferChecker::check(const void* p, uint64_t bytes, const char* what, int idx) {
+  if (bytes == 0) return ARK_OPT_OK;
+  const uintptr_t q = (uintptr_t)p;
+  for (int i = 0; i < used_; ++i)
+    if (p != nullptr && q >= base_[i] && q - base_[i] <= size_[i] &&
+        bytes <= size_[i] - (q - base_[i]))
+      return ARK_OPT_OK;
+  uintptr_t b;
+  size_t s;
+  const int rc = check_buffer_range(p, bytes, what, idx, &b, &s);
+  if (rc == ARK_OPT_OK && s != 0) {
+    base_[next_] = b;
+    size_[next_] = s;
+    next_ = (next_ + 1) % kRanges;
+    if (used_ < kRanges) ++used_;
+  }
+  return rc;
 }
 
 DeviceGuard::DeviceGuard(int dev) {

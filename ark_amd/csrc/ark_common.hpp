@@ -27,6 +27,20 @@ const char* last_error();
 // before any kernel touches them.  what/idx name the buffer in the message.
 int check_buffer(const void* p, uint64_t bytes, const char* what, int idx);
 
+// check_buffer for many buffers that mostly share a few allocations (one
+// arena per array kind): an allocation range found once is remembered, and a
+// buffer inside a remembered range needs no runtime query.
+class BufferChecker {
+ public:
+  int check(const void* p, uint64_t bytes, const char* what, int idx);
+
+ private:
+  static constexpr int kRanges = 8;
+  uintptr_t base_[kRanges] = {};
+  size_t size_[kRanges] = {};
+  int used_ = 0, next_ = 0;
+};
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
   int prev = -1;

@@ -197,12 +197,13 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
+  ark::BufferChecker checker;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
-    if ((rc = check_buffer(t.w, t.n * 2u, "w", i))) return rc;
-    if ((rc = check_buffer(t.g, t.n * gsz, "g", i))) return rc;
-    if ((rc = check_buffer(t.m, t.n * 4u, "m", i))) return rc;
-    if ((rc = check_buffer(t.v, t.n * 4u, "v", i))) return rc;
+    if ((rc = checker.check(t.w, t.n * 2u, "w", i))) return rc;
+    if ((rc = checker.check(t.g, t.n * gsz, "g", i))) return rc;
+    if ((rc = checker.check(t.m, t.n * 4u, "m", i))) return rc;
+    if ((rc = checker.check(t.v, t.n * 4u, "v", i))) return rc;
   }
 
   ark_opt_handle* h = new ark_opt_handle();

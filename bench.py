@@ -242,6 +242,89 @@ def run_codec(a):
     print(json.dumps(out), flush=True)
 
 
+def run_ckpt(a):
+    """Checkpoint V4 of EKO-237M (include/ark_ckpt.h): the 816-record file
+    image (2.37 GB: fp16 w, fp32 m/v) packed from the device buffers and
+    unpacked back, in device memory (2 B of traffic per image byte each
+    way), then the whole file written and read through the host."""
+    import tempfile
+    import torch
+    from ark_amd import ckpt
+    from ark_amd.eko import EKO_237M
+    from ark_amd.optimizer import ParamSet
+    torch.cuda.set_device(0)
+    ps = ParamSet(EKO_237M.tensors(), weight_decay=0.1)
+    tens = ckpt.param_tensors(ps)
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+    for t in tens:
+        t.copy_(torch.randn(t.shape, device="cuda", generator=g) * 0.02)
+    recs = ckpt.Records(tens)
+    nb = ckpt.image_bytes(recs)
+    img = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    res = {}
+    steps = max(1, min(a.steps, 50))
+    for name, fn in (("pack", lambda: ckpt.pack(recs, img, 1000, 999)),
+                     ("unpack", lambda: ckpt.unpack(img, recs))):
+        for _ in range(min(a.warmup, 5)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = dict(ms=e0.elapsed_time(e1) / steps,
+                         wall_ms=(time.perf_counter() - t0) * 1e3 / steps)
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    path = os.path.join(d, f"ark_bench_ckpt_{os.getpid()}.bin")
+    try:
+        t0 = time.perf_counter()
+        ckpt.save(path, recs, 1000, 999)
+        save_s = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        ckpt.load(path, recs)
+        load_s = time.perf_counter() - t0
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    cpu = None
+    if not a.no_cpu:
+        import numpy as np
+        from oracle import ckpt as K
+        host = [t.cpu().numpy() for t in tens[:30]]  # embed w/m/v + layer 0's 27 records
+        reps, t0 = 0, time.perf_counter()
+        nbytes = 0
+        while time.perf_counter() - t0 < min(a.cpu_seconds, 10.0):
+            nbytes += len(K.write_v4(1000, 999, host))
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(2 * nbytes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                   sample=f"{reps} V4 images of embed + layer 0 ({nbytes // reps} B each) built "
+                          f"by the oracle writer in {el:.1f} s")
+    pk = 2 * nb / (res["pack"]["ms"] * 1e-3) / 1e9
+    up = 2 * nb / (res["unpack"]["ms"] * 1e-3) / 1e9
+    out = {
+        "metric": "EKO-237M checkpoint V4 pack from device buffers, GB/s of HBM traffic (1 GPU)",
+        "value": round(pk, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": min(a.warmup, 5), "ms_per_step": round(res["pack"]["ms"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "ckpt: EKO-237M V4 image, 816 records", "image_bytes": nb,
+                   "unpack_ms": round(res["unpack"]["ms"], 4), "unpack_GBs": round(up, 2),
+                   "pack_call_wall_ms": round(res["pack"]["wall_ms"], 3),
+                   "save_file_s": round(save_s, 3), "save_file_GBs": round(nb / save_s / 1e9, 2),
+                   "load_file_s": round(load_s, 3), "load_file_GBs": round(nb / load_s / 1e9, 2),
+                   "file_dir": d},
+        "roofline": {"kernel": "pack_kernel", "bound": "hbm", "achieved": round(pk, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pk / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": 2 * nb},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,8 +334,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", default="step", choices=["step", "codec"],
-                    help="step: the optimizer step (headline); codec: the weight codec")
+    ap.add_argument("--path", default="step", choices=["step", "codec", "ckpt"],
+                    help="step: the optimizer step (headline); codec: the weight codec; "
+                         "ckpt: the V4 checkpoint image")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -262,6 +346,9 @@ def main():
         sys.exit(2)
     if a.path == "codec":
         run_codec(a)
+        return
+    if a.path == "ckpt":
+        run_ckpt(a)
         return
 
     r = run_gpu(a.workload, a.steps, a.warmup)

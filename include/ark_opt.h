@@ -41,6 +41,7 @@ extern "C" {
 #define ARK_OPT_EINVAL (-1) /* bad argument (null pointer, size, alignment) */
 #define ARK_OPT_EHIP (-2)   /* a HIP runtime call failed */
 #define ARK_OPT_ENOMEM (-3) /* device or pinned allocation failed */
+#define ARK_OPT_EIO (-4)    /* a file could not be read or written, or is malformed */
 
 /* ---- norm definition --------------------------------------------------- */
 /* The global sum of squares is a pairwise (index-order binary tree) f64 sum

@@ -1,0 +1,221 @@
+"""GPU parity of the checkpoint path (include/ark_ckpt.h) against the
+checkpoint oracle (oracle/ckpt.py, the format of io.rs:432-671): files
+written from device buffers equal the oracle's bytes, files the oracle
+writes (V4, V3, V2) load into device buffers as the reference's chain of
+conversions would, and the full EKO-237M image packs and unpacks bit for
+bit."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import ckpt as K
+from ark_amd import _abi, ckpt
+from ark_amd._lib import ArkOptError
+from ark_amd.eko import EKO_237M, EkoConfig
+
+pytestmark = pytest.mark.gpu
+
+ODD = EkoConfig(n_layers=2, d_model=33, hidden=47, vocab=101)  # odd sizes: unaligned records
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return torch
+
+
+def _bits(t):
+    torch = _torch()
+    it = {2: torch.int16, 4: torch.int32}[t.element_size()]
+    u = {2: np.uint16, 4: np.uint32}[t.element_size()]
+    return t.view(it).cpu().numpy().view(u)
+
+
+def _fill_random(tensors, seed):
+    """Every bit pattern equally likely: NaNs, infinities, subnormals."""
+    torch = _torch()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for t in tensors:
+        if t.element_size() == 2:
+            t.view(torch.int16).copy_(torch.randint(-32768, 32768, t.shape, device="cuda",
+                                                    generator=g, dtype=torch.int32))
+        else:
+            t.view(torch.int32).copy_(torch.randint(-2 ** 31, 2 ** 31, t.shape, device="cuda",
+                                                    generator=g, dtype=torch.int64))
+
+
+def _quiet16(h):
+    h = h.copy()
+    snan = ((h & 0x7C00) == 0x7C00) & ((h & 0x03FF) != 0)
+    h[snan] |= 0x0200
+    return h
+
+
+def _params(cfg, seed):
+    from ark_amd.optimizer import ParamSet
+    ps = ParamSet(cfg.tensors(), weight_decay=0.1)
+    _fill_random(ckpt.param_tensors(ps), seed)
+    return ps
+
+
+def _oracle_bytes(ps, global_step, adam_step):
+    t = [_bits(x) for x in ckpt.param_tensors(ps)]
+    nl = (len(t) - 6) // 27
+    lw = [t[3 + 27 * l: 12 + 27 * l] for l in range(nl)]
+    lm = [t[12 + 27 * l: 21 + 27 * l] for l in range(nl)]
+    lv = [t[21 + 27 * l: 30 + 27 * l] for l in range(nl)]
+    return K.save_fp16(global_step, adam_step, t[0], t[1].view(np.float32), t[2].view(np.float32),
+                       t[-3], t[-2].view(np.float32), t[-1].view(np.float32), lw,
+                       [[a.view(np.float32) for a in l] for l in lm],
+                       [[a.view(np.float32) for a in l] for l in lv])
+
+
+def test_save_equals_oracle_bytes(tmp_path):
+    torch = _torch()
+    ps = _params(ODD, 1)
+    st = _abi.State(t=37, loss_scale=4096.0, clean_steps=12, consecutive_nonfinite=0,
+                    skipped_steps=5, early_stop=0, reserved=0)
+    p = str(tmp_path / "a.bin")
+    ckpt.save(p, ckpt.param_tensors(ps), 1234, 37, st)
+    got = open(p, "rb").read()
+    want = _oracle_bytes(ps, 1234, 37) + K.amp_trailer(bytes(st))
+    assert len(got) == len(want)
+    assert got == want
+    # without the trailer: exactly the reference's file
+    ckpt.save(p, ckpt.param_tensors(ps), 1234, 37)
+    assert open(p, "rb").read() == want[:-40]
+    torch.cuda.synchronize()
+
+
+def test_round_trip_through_file(tmp_path):
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    ps = _params(ODD, 2)
+    opt = Optimizer(AdamConfig(), ps, AmpConfig(loss_scale_init=1024.0))
+    opt.set_state(t=99, loss_scale=2048.0, clean_steps=17, skipped_steps=3)
+    p = str(tmp_path / "b.bin")
+    ckpt.save_params(p, ps, opt, global_step=500)
+    info, pairs = ckpt.probe(p)
+    assert (info.version, info.global_step, info.adam_step, info.has_amp) == (4, 500, 99, True)
+    assert info.n_tensors == 3 + 27 * 2 + 3 == len(pairs)
+    qs = ParamSet(ODD.tensors(), weight_decay=0.1)
+    opt2 = Optimizer(AdamConfig(), qs, AmpConfig(loss_scale_init=1024.0))
+    ckpt.load_params(p, qs, opt2)
+    for a, b in zip(ckpt.param_tensors(ps), ckpt.param_tensors(qs)):
+        want = _bits(a)
+        if a.element_size() == 2:
+            want = _quiet16(want)  # half::to_f32 then fcvtn quiets signalling NaNs
+        np.testing.assert_array_equal(_bits(b), want)
+    s1, s2 = opt.get_state(), opt2.get_state()
+    for k in ("t", "loss_scale", "clean_steps", "consecutive_nonfinite", "skipped_steps"):
+        assert getattr(s1, k) == getattr(s2, k), k
+    opt.close(), opt2.close()
+
+
+def test_load_oracle_v4_into_f32(tmp_path):
+    """CheckpointV3::load's pesos are fp32: F16 records widen exactly."""
+    torch = _torch()
+    rng = np.random.default_rng(4)
+    tens = [rng.integers(0, 65536, n, dtype=np.uint32).astype(np.uint16) for n in (1, 5, 4096, 4099)]
+    tens += [rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+             for n in (3, 8191)]
+    p = str(tmp_path / "c.bin")
+    open(p, "wb").write(K.write_v4(7, 8, tens))
+    outs = [torch.empty(t.size, dtype=torch.float32, device="cuda") for t in tens]
+    info, amp = ckpt.load(p, outs)
+    assert amp is None and info.adam_step == 8
+    for t, o in zip(tens, outs):
+        want = oracle.f16_to_f32(t).view(np.uint32) if t.dtype == np.uint16 else t.view(np.uint32)
+        np.testing.assert_array_equal(_bits(o), want)
+
+
+@pytest.mark.parametrize("version", [3, 2])
+def test_load_oracle_v3_v2_into_fp16_weights(tmp_path, version):
+    """V3 / V2 weights are fp32: into fp16 buffers they round to nearest
+    even (sync_weights_to_gpu's ark_quant_f32_to_f16, memory.rs:347-377)."""
+    torch = _torch()
+    rng = np.random.default_rng(version)
+    ns = [7, 4096, 12345, 33]
+    tens = [rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+            for n in ns]
+    data = K.write_v3(5, 6, tens) if version == 3 else K.write_v2(5, tens)
+    p = str(tmp_path / "d.bin")
+    open(p, "wb").write(data)
+    info, pairs = ckpt.probe(p)
+    assert info.version == version and [n for n, _ in pairs] == ns
+    assert all(t == _abi.CKPT_F32 for _, t in pairs)
+    outs = [torch.empty(n, dtype=torch.float16 if i % 2 == 0 else torch.float32, device="cuda")
+            for i, n in enumerate(ns)]
+    info, _ = ckpt.load(p, outs)
+    assert info.has_moments == (version == 3) and info.adam_step == (6 if version == 3 else 0)
+    for t, o in zip(tens, outs):
+        want = oracle.f32_to_f16(t) if o.element_size() == 2 else t.view(np.uint32)
+        np.testing.assert_array_equal(_bits(o), want)
+
+
+def test_full_eko237m_image():
+    """Pack the 816-record EKO-237M checkpoint (2.37 GB) on the device: the
+    image equals the oracle's file bytes; unpacking it restores every
+    buffer."""
+    torch = _torch()
+    from ark_amd.optimizer import ParamSet
+    ps = _params(EKO_237M, 3)
+    tens = ckpt.param_tensors(ps)
+    nb = ckpt.image_bytes(tens)
+    img = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    ckpt.pack(tens, img, 4000, 3999)
+    got = img.cpu().numpy()
+    want = np.frombuffer(_oracle_bytes(ps, 4000, 3999), np.uint8)
+    assert got.size == want.size
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[0]}"
+    del got, want
+    qs = ParamSet(EKO_237M.tensors(), weight_decay=0.1)
+    ckpt.unpack(img, ckpt.param_tensors(qs))
+    for a, b in zip(tens, ckpt.param_tensors(qs)):
+        if a.element_size() == 4:
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        else:
+            np.testing.assert_array_equal(_bits(b), _quiet16(_bits(a)))
+
+
+def test_rejects_bad_files(tmp_path):
+    torch = _torch()
+    x = [torch.zeros(5, dtype=torch.float16, device="cuda"),
+         torch.zeros(3, dtype=torch.float32, device="cuda")]
+    p = str(tmp_path / "e.bin")
+    open(p, "wb").write(b"\x12\x34\x56\x78" + b"\0" * 60)
+    with pytest.raises(ArkOptError, match="bad magic"):
+        ckpt.load(p, x)
+    good = K.write_v4(1, 1, [np.zeros(5, np.uint16), np.zeros(3, np.float32)])
+    open(p, "wb").write(good[:-1])
+    with pytest.raises(ArkOptError, match="truncated"):
+        ckpt.load(p, x)
+    open(p, "wb").write(good)
+    with pytest.raises(ArkOptError, match="2 tensors, 1 records"):
+        ckpt.load(p, x[:1])
+    with pytest.raises(ArkOptError, match="n=5"):
+        ckpt.load(p, [x[0][:4], x[1]])
+    ckpt.load(p, x)  # and the good file loads
+    with pytest.raises(ArkOptError):
+        ckpt.load(str(tmp_path / "missing.bin"), x)
+
+
+def test_unpack_checks_headers():
+    torch = _torch()
+    x = [torch.arange(9, dtype=torch.float16, device="cuda"),
+         torch.arange(4, dtype=torch.float32, device="cuda")]
+    img = torch.empty(ckpt.image_bytes(x), dtype=torch.uint8, device="cuda")
+    ckpt.pack(x, img, 1, 2)
+    y = [torch.empty_like(t) for t in x]
+    ckpt.unpack(img, y)
+    assert all(torch.equal(a, b) for a, b in zip(x, y))
+    img[28 + 16 + 18] ^= 1  # second record's n
+    with pytest.raises(ArkOptError, match="tensor 1 header"):
+        ckpt.unpack(img, y)
+    img[28 + 16 + 18] ^= 1
+    img[0] ^= 1
+    with pytest.raises(ArkOptError, match="file header"):
+        ckpt.unpack(img, y)
