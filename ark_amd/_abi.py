@@ -127,3 +127,8 @@ class CkptInfo(C.Structure):
                 ("global_step", C.c_uint64), ("adam_step", C.c_uint64),
                 ("n_tensors", C.c_uint64), ("file_bytes", C.c_uint64),
                 ("has_amp", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+# include/ark_grad.h
+class GradSpan(C.Structure):
+    _fields_ = [("dst", C.c_void_p), ("src", C.c_void_p), ("n", C.c_uint64)]

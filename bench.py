@@ -325,6 +325,83 @@ def run_ckpt(a):
     print(json.dumps(out), flush=True)
 
 
+def run_grad(a):
+    """The gradient hand-off of EKO-237M (include/ark_grad.h): one launch
+    adding all 272 backward outputs into the fp32 gradients (12 B/param:
+    two reads, one write), and the token scatter of a 2 x 2048-token batch
+    (config.rs:62-67) into the 32000 x 768 embedding gradient."""
+    import numpy as np
+    import torch
+    from ark_amd import grad
+    from ark_amd.eko import EKO_237M
+    torch.cuda.set_device(0)
+    specs = EKO_237M.tensors()
+    n = sum(s.n for s in specs)
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+    dst = [torch.randn(s.n, device="cuda", generator=g) for s in specs]
+    src = [torch.randn(s.n, device="cuda", generator=g) for s in specs]
+    plan = grad.GradPlan(list(zip(dst, src)))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(a.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        plan.run()
+    e1.record()
+    torch.cuda.synchronize()
+    acc_ms = e0.elapsed_time(e1) / a.steps
+    plan.close()
+    vocab, d, bs = 32000, 768, 4096
+    rng = np.random.default_rng(SEED)
+    tokens = torch.from_numpy(((rng.zipf(1.2, bs) - 1) % vocab).astype(np.int32)).cuda()
+    dx0 = torch.randn(bs, d, device="cuda", generator=g)
+    eg = dst[0].view(vocab, d)
+    for _ in range(a.warmup):
+        grad.embed_scatter(eg, tokens, dx0)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        grad.embed_scatter(eg, tokens, dx0)
+    e1.record()
+    torch.cuda.synchronize()
+    sc_ms = e0.elapsed_time(e1) / a.steps
+    uniq = int(torch.unique(tokens).numel())
+    cpu = None
+    if not a.no_cpu:
+        import oracle
+        from concurrent.futures import ThreadPoolExecutor
+        th = a.cpu_threads or min(16, os.cpu_count() or 1)
+        hd = dst[0].cpu().numpy()
+        hs = src[0].cpu().numpy()
+        parts = list(zip(np.array_split(hd, th), np.array_split(hs, th)))
+        reps, t0 = 0, time.perf_counter()
+        with ThreadPoolExecutor(th) as ex:
+            while time.perf_counter() - t0 < min(a.cpu_seconds, 10.0):
+                list(ex.map(lambda p: oracle.grad_accumulate(*p), parts))
+                reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(12 * hd.size * reps / el / 1e9, 3), unit="GB/s", cores=th,
+                   kind="port", sample=f"{reps} accumulations of the {hd.size}-element "
+                   f"embedding gradient in {el:.1f} s on {th} threads")
+    gbs = 12 * n / (acc_ms * 1e-3) / 1e9
+    out = {
+        "metric": "EKO-237M gradient accumulation (all tensors, fp32 +=) GB/s (1 GPU)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(acc_ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "grad: 272 EKO-237M fp32 gradient buffers += backward outputs; "
+                               "token scatter of 4096 tokens (Zipf 1.2) into 32000 x 768",
+                   "elements": n, "bytes_per_launch": 12 * n,
+                   "scatter_ms": round(sc_ms, 4), "scatter_unique_tokens": uniq},
+        "roofline": {"kernel": "grad_batch", "bound": "hbm", "achieved": round(gbs, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": 12 * n},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -334,9 +411,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", default="step", choices=["step", "codec", "ckpt"],
+    ap.add_argument("--path", default="step", choices=["step", "codec", "ckpt", "grad"],
                     help="step: the optimizer step (headline); codec: the weight codec; "
-                         "ckpt: the V4 checkpoint image")
+                         "ckpt: the V4 checkpoint image; grad: the gradient hand-off")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -349,6 +426,9 @@ def main():
         return
     if a.path == "ckpt":
         run_ckpt(a)
+        return
+    if a.path == "grad":
+        run_grad(a)
         return
 
     r = run_gpu(a.workload, a.steps, a.warmup)

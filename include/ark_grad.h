@@ -1,0 +1,62 @@
+/*
+ * ark_grad.h -- the gradient hand-off into the optimizer step, on MI355X
+ * (gfx950).
+ *
+ * Replaces the host tail of ark_mps_backward (proyecto_ark/ark01/objc/
+ * bridge.m:902-948): after the backward pass the reference waits for the
+ * device (:902-905) and then, on the CPU, adds every parameter-gradient
+ * buffer into the Rust-side fp32 gradients (`+=`, :931-947), the LM-head
+ * gradient into the tied embedding gradient (:910-911), gamma_final's
+ * (:914-915), and scatter-adds each row of dL/d(embedding output) into the
+ * embedding row of its token (:922-928).  Here the same sums run on the
+ * device, stream ordered, with no host wait; the results are bit-identical
+ * to those loops (fp32 adds in the same order), and the fp32 gradients they
+ * produce go straight to ark_opt_step with ARK_OPT_GRAD_F32.
+ *
+ * Every function returns an ARK_OPT_* status code (include/ark_opt.h) with
+ * the message in ark_opt_last_error().  Pointers are device pointers.
+ */
+#ifndef ARK_GRAD_H
+#define ARK_GRAD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dst[i] = dst[i] + src[i] for i < n (bridge.m:910-915, :931-947). */
+typedef struct ark_grad_span {
+  float *dst;
+  const float *src;
+  uint64_t n;
+} ark_grad_span;
+
+/* One span, one launch.  dst and src must not overlap. */
+int ark_grad_accumulate(float *dst, const float *src, uint64_t n, void *stream);
+
+/* Every span of a model in one launch; the plan copies the span table to
+ * the device once.  Spans must not overlap each other's dst. */
+typedef struct ark_grad_plan ark_grad_plan;
+int ark_grad_plan_create(const ark_grad_span *spans, int32_t n_spans, void *stream,
+                         ark_grad_plan **out);
+int ark_grad_plan_run(ark_grad_plan *plan);
+int ark_grad_plan_destroy(ark_grad_plan *plan);
+
+/* bridge.m:922-928: for i in [0, batch_seq) in order, with
+ * t = tokens[i] < vocab ? tokens[i] : 0,
+ *     embed_grad[t*d + j] += dx0[i*d + j]   for j < d.
+ * Every element receives its additions in increasing i, as in the loop: the
+ * positions are stably sorted by token on the device and one wave adds each
+ * token's rows in order.  embed_grad holds vocab*d floats, dx0 batch_seq*d,
+ * tokens batch_seq.  Stream ordered; the scratch it needs (16 B per token
+ * plus the sort's) comes from the stream-ordered pool. */
+int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
+                           const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
+                           void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARK_GRAD_H */

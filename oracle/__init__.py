@@ -54,6 +54,10 @@ def lib():
     L.ark_ref_compare_f32_to_f16_range.argtypes = [C.c_uint64, C.c_uint64, P, C.c_int,
                                                    C.POINTER(C.c_uint64)]
     L.ark_ref_compare_f32_to_f16_range.restype = C.c_int64
+    L.ark_ref_grad_accumulate.argtypes = [P, P, C.c_uint64]
+    L.ark_ref_grad_accumulate.restype = None
+    L.ark_ref_embed_scatter.argtypes = [P, C.c_uint32, C.c_uint32, P, P, C.c_uint32]
+    L.ark_ref_embed_scatter.restype = None
     L.ark_ref_pow_binary.argtypes = [C.c_float, C.c_uint32]
     L.ark_ref_pow_binary.restype = C.c_float
     L.ark_ref_prologue.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float,
@@ -122,6 +126,25 @@ def compare_f32_to_f16_range(lo, got, nthreads=8):
     bad = lib().ark_ref_compare_f32_to_f16_range(lo, lo + got.size, _ptr(got), nthreads,
                                                  C.byref(first))
     return bad, (None if first.value == 2 ** 64 - 1 else first.value)
+
+
+def grad_accumulate(dst, src):
+    """In place: dst (float32) += src (float32), i ascending."""
+    assert dst.dtype == np.float32 and src.dtype == np.float32 and dst.flags.c_contiguous
+    src = np.ascontiguousarray(src)
+    assert dst.size == src.size
+    lib().ark_ref_grad_accumulate(_ptr(dst), _ptr(src), dst.size)
+
+
+def embed_scatter(embed_grad, tokens, dx0):
+    """In place on embed_grad (vocab x d float32): the loop of
+    objc/bridge.m:922-928 over tokens (uint32) and dx0 (batch x d float32)."""
+    assert embed_grad.dtype == np.float32 and embed_grad.flags.c_contiguous
+    vocab, d = embed_grad.shape
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    dx0 = np.ascontiguousarray(dx0, dtype=np.float32)
+    assert dx0.shape == (tokens.size, d)
+    lib().ark_ref_embed_scatter(_ptr(embed_grad), vocab, d, _ptr(tokens), _ptr(dx0), tokens.size)
 
 
 def pow_binary(beta, t):

@@ -655,3 +655,20 @@ void ark_ref_synth_normal_f16(uint16_t *out, uint64_t n, uint64_t seed,
   for (uint64_t i = 0; i < n; ++i)
     out[i] = ark_ref_f32_to_f16(synth_z(base, i) * sigma_scale);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Gradient hand-off (objc/bridge.m:902-948).                                */
+/* ------------------------------------------------------------------------ */
+
+void ark_ref_grad_accumulate(float *dst, const float *src, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) dst[i] += src[i];
+}
+
+void ark_ref_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
+                           const uint32_t *tokens, const float *dx0, uint32_t batch_seq) {
+  for (uint32_t i = 0; i < batch_seq; ++i) {
+    uint32_t t = (tokens[i] < vocab) ? tokens[i] : 0;
+    for (uint32_t j = 0; j < d; ++j)
+      embed_grad[(uint64_t)t * d + j] += dx0[(uint64_t)i * d + j];
+  }
+}

@@ -115,6 +115,18 @@ void ark_ref_synth_normal_f16(uint16_t *out, uint64_t n, uint64_t seed,
                               uint32_t tensor_id, uint32_t step,
                               float sigma_scale);
 
+/* ------------------------------------------------------------------------ */
+/* Gradient hand-off (objc/bridge.m:902-948).                                */
+/* ------------------------------------------------------------------------ */
+
+/* dst[i] += src[i], i ascending (bridge.m:910-915, :931-947). */
+void ark_ref_grad_accumulate(float *dst, const float *src, uint64_t n);
+
+/* bridge.m:922-928, literally: for i < batch_seq, t = tokens[i] < vocab ?
+ * tokens[i] : 0, then embed_grad[t*d + j] += dx0[i*d + j] for j < d. */
+void ark_ref_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
+                           const uint32_t *tokens, const float *dx0, uint32_t batch_seq);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,164 @@
+"""GPU parity of the gradient hand-off (include/ark_grad.h) against the
+oracle's literal restatement of the CPU loops of objc/bridge.m:902-948:
+fp32 accumulation of every gradient buffer, the LM-head and gamma_final
+adds, and the token scatter-add into the embedding gradient with the loop's
+summation order; then the produced fp32 gradients through ark_opt_step
+against the oracle's optimizer."""
+import numpy as np
+import pytest
+
+import oracle
+from ark_amd import grad
+from ark_amd.eko import EKO_237M
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return torch
+
+
+def _bits(t):
+    torch = _torch()
+    return t.view(torch.int32).cpu().numpy().view(np.uint32)
+
+
+def _zipf_tokens(rng, n, vocab, extra=0):
+    t = (rng.zipf(1.2, n) - 1) % (vocab + extra)
+    return t.astype(np.uint32)
+
+
+@pytest.mark.parametrize("vocab,d,n,extra", [(32000, 768, 4096, 0), (32000, 768, 4096, 50),
+                                             (1000, 33, 777, 10), (5, 64, 2000, 2),
+                                             (32000, 768, 1, 0)])
+def test_scatter_matches_oracle(vocab, d, n, extra):
+    torch = _torch()
+    rng = np.random.default_rng(vocab + d + n)
+    tokens = _zipf_tokens(rng, n, vocab, extra)
+    dx0 = (rng.standard_normal((n, d)) * 10.0 ** rng.integers(-6, 3, (n, 1))).astype(np.float32)
+    g = rng.standard_normal((vocab, d)).astype(np.float32)
+    want = g.copy()
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.from_numpy(g).cuda()
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    got = _bits(gg).reshape(vocab, d)
+    bad = np.argwhere(got != want.view(np.uint32))
+    assert bad.size == 0, f"{len(bad)} elements differ, first {bad[0].tolist()}"
+
+
+def test_scatter_one_long_run_and_order():
+    """Every position the same token: one run of 4096 rows added in order;
+    plus the order-revealing values (1e8, 1, -1e8, 1)."""
+    torch = _torch()
+    vocab, d, n = 100, 256, 4096
+    rng = np.random.default_rng(7)
+    dx0 = rng.standard_normal((n, d)).astype(np.float32)
+    dx0[:4, :] = np.array([1e8, 1.0, -1e8, 1.0], np.float32)[:, None]
+    tokens = np.full(n, 42, np.uint32)
+    want = np.zeros((vocab, d), np.float32)
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.zeros(vocab, d, device="cuda")
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
+def test_scatter_unaligned_rows_take_the_scalar_path():
+    torch = _torch()
+    vocab, d, n = 300, 64, 500
+    rng = np.random.default_rng(8)
+    tokens = _zipf_tokens(rng, n, vocab)
+    base = torch.from_numpy(rng.standard_normal(n * d + 1).astype(np.float32)).cuda()
+    dx0 = base[1:].view(n, d)  # 4-byte, not 16-byte, aligned
+    want = np.zeros((vocab, d), np.float32)
+    oracle.embed_scatter(want, tokens, dx0.cpu().numpy())
+    gg = torch.zeros(vocab, d, device="cuda")
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(), dx0)
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
+def test_accumulate_and_plan_eko237m():
+    """All 272 EKO-237M fp32 gradient buffers += their backward outputs in
+    one launch, against torch's fp32 add (an independent reference of an
+    elementwise IEEE add) and the oracle on the small tensors."""
+    torch = _torch()
+    specs = EKO_237M.tensors()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    dst = [torch.randn(s.n, device="cuda", generator=g) for s in specs]
+    src = [torch.randn(s.n, device="cuda", generator=g) * 1e-3 for s in specs]
+    want = [a + b for a, b in zip(dst, src)]
+    small = [(i, dst[i].cpu().numpy().copy(), src[i].cpu().numpy()) for i, s in enumerate(specs)
+             if s.n <= 768 * 2048][:12]
+    plan = grad.GradPlan(list(zip(dst, src)))
+    plan.run()
+    torch.cuda.synchronize()
+    for a, w in zip(dst, want):
+        assert torch.equal(a.view(torch.int32), w.view(torch.int32))
+    for i, a, b in small:
+        oracle.grad_accumulate(a, b)
+        np.testing.assert_array_equal(_bits(dst[i]), a.view(np.uint32))
+    plan.close()
+    x = torch.randn(4099, device="cuda")
+    y = torch.randn(4100, device="cuda")[1:]  # unaligned source
+    w = x + y
+    grad.accumulate(x, y)
+    torch.cuda.synchronize()
+    assert torch.equal(x, w)
+
+
+def test_handoff_into_optimizer_step():
+    """The backward tail on the device feeding ark_opt_step (fp32 grads):
+    every gradient buffer += its backward output (the LM-head add is the
+    embedding's), then the token scatter, then one AMP + clip + AdamW step;
+    gradients, step scalars and w/m/v against the oracle's loops and
+    optimizer, bit for bit."""
+    torch = _torch()
+    from ark_amd import _abi
+    from ark_amd.eko import EkoConfig
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    from oracle import harness as H
+
+    cfg = EkoConfig(n_layers=2, d_model=64, hidden=96, vocab=500)
+    specs = cfg.tensors()
+    rng = np.random.default_rng(11)
+    scale = 1024.0
+    ps = ParamSet(specs, weight_decay=0.1, grad_dtype=_abi.GRAD_F32)
+    w0 = [(rng.standard_normal(s.n) * 0.02).astype(np.float16) for s in specs]
+    for i in range(len(specs)):
+        ps.w(i).copy_(torch.from_numpy(w0[i]))
+    outs = [(rng.standard_normal(s.n) * 1e-3 * scale).astype(np.float32) for s in specs]
+    n_tok = 300
+    tokens = _zipf_tokens(rng, n_tok, cfg.vocab, 3)
+    dx0 = (rng.standard_normal((n_tok, cfg.d_model)) * 1e-3 * scale).astype(np.float32)
+    e = [s.name for s in specs].index("embed")
+    # device: grads start at zero (training.rs:248), += outputs, then the scatter
+    dev_out = [torch.from_numpy(o).cuda() for o in outs]
+    plan = grad.GradPlan([(ps.g(i), dev_out[i]) for i in range(len(specs))])
+    plan.run()
+    grad.embed_scatter(ps.g(e).view(cfg.vocab, cfg.d_model),
+                       torch.from_numpy(tokens.view(np.int32)).cuda(), torch.from_numpy(dx0).cuda())
+    acfg = AdamConfig(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
+    opt = Optimizer(acfg, ps, AmpConfig(loss_scale_init=scale))
+    _, gi = opt.step_all(3e-4, info=True)
+    # host: the same loops, then the oracle optimizer on the same inputs
+    host_g = [np.zeros(s.n, np.float32) for s in specs]
+    for h, o in zip(host_g, outs):
+        oracle.grad_accumulate(h, o)
+    oracle.embed_scatter(host_g[e].reshape(cfg.vocab, cfg.d_model), tokens, dx0)
+    for i in range(len(specs)):
+        np.testing.assert_array_equal(_bits(ps.g(i)), host_g[i].view(np.uint32))
+    ts = [oracle.HostTensor(w0[i].view(np.uint16).copy(), host_g[i], np.zeros(s.n, np.float32),
+                            np.zeros(s.n, np.float32), 0.1 if s.decay else 0.0)
+          for i, s in enumerate(specs)]
+    ref = oracle.Optimizer(ts, opt.hp)
+    _, ri = ref.step(3e-4)
+    d = H.info_matches(gi, ri)
+    assert not d, d
+    assert gi.applied == 1
+    c = H.compare(ps, ts)
+    assert c["w"] == 0 and c["m"] == 0 and c["v"] == 0, c
+    opt.close()
+    plan.close()
