@@ -158,11 +158,11 @@ def run_cpu_baseline(name, budget_s, threads):
                        f"threads of {os.cpu_count()} ({cpu})")
 
 
-def traffic_from_profiles(name):
-    """HBM-side bytes per adamw_kernel launch measured by rocprofv3 byte
+def traffic_from_profiles(name, kernel="adamw_kernel"):
+    """HBM-side bytes per launch of `kernel` measured by rocprofv3 byte
     counters (calibrated against a plain copy) for this workload, from the
     committed profile summary; None when no profile of it is committed."""
-    p = os.path.join(ROOT, "profiles", f"adamw_kernel_{name}_traffic.txt")
+    p = os.path.join(ROOT, "profiles", f"{kernel}_{name}_traffic.txt")
     if not os.path.exists(p):
         return None, None
     kv = {}
@@ -236,7 +236,9 @@ def run_codec(a):
                    "quant_ms": round(res["quant"]["ms"], 4), "quant_GBs": round(q_gbs, 2)},
         "roofline": {"kernel": "codec_batch<f16_to_f32>", "bound": "hbm", "achieved": round(gbs, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": 6 * n},
+                     "traffic": traffic_from_profiles("eko237m", "codec_batch")[0],
+                     "traffic_source": traffic_from_profiles("eko237m", "codec_batch")[1],
+                     "algorithmic_bytes_per_launch": 6 * n},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -319,7 +321,9 @@ def run_ckpt(a):
                    "file_dir": d},
         "roofline": {"kernel": "pack_kernel", "bound": "hbm", "achieved": round(pk, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pk / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": 2 * nb},
+                     "traffic": traffic_from_profiles("eko237m", "pack_kernel")[0],
+                     "traffic_source": traffic_from_profiles("eko237m", "pack_kernel")[1],
+                     "algorithmic_bytes_per_launch": 2 * nb},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -396,7 +400,9 @@ def run_grad(a):
                    "scatter_ms": round(sc_ms, 4), "scatter_unique_tokens": uniq},
         "roofline": {"kernel": "grad_batch", "bound": "hbm", "achieved": round(gbs, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": 12 * n},
+                     "traffic": traffic_from_profiles("eko237m", "grad_batch")[0],
+                     "traffic_source": traffic_from_profiles("eko237m", "grad_batch")[1],
+                     "algorithmic_bytes_per_launch": 12 * n},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -421,14 +427,10 @@ def main():
         print("bench.py measures one GPU only: the optimizer step of this build runs on a "
               "single MI355X (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    if a.path == "codec":
-        run_codec(a)
-        return
-    if a.path == "ckpt":
-        run_ckpt(a)
-        return
-    if a.path == "grad":
-        run_grad(a)
+    if a.path != "step":
+        {"codec": run_codec, "ckpt": run_ckpt, "grad": run_grad}[a.path](a)
+        if a.calib_copy:
+            calib_copy()
         return
 
     r = run_gpu(a.workload, a.steps, a.warmup)
