@@ -23,13 +23,16 @@
 //
 // All HBM bound: 2 bytes of traffic per image byte (one read, one write).
 // Files move through two pinned staging buffers, copy and file I/O
-// overlapped.
+// overlapped, each chunk's file I/O split over several threads.
 #include <errno.h>
 #include <fcntl.h>
 #include <string.h>
+#include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <string>
+#include <thread>
 #include <vector>
 
 #include "ark_ckpt.h"
@@ -344,6 +347,13 @@ struct StreamSync {
   hipStream_t s;
   ~StreamSync() { (void)hipStreamSynchronize(s); }
 };
+struct FileMap {
+  uint8_t* p = nullptr;
+  uint64_t len = 0;
+  ~FileMap() {
+    if (p) (void)munmap(p, len);
+  }
+};
 struct Fd {
   int fd = -1;
   ~Fd() {
@@ -544,17 +554,76 @@ int read_exact(int fd, void* buf, uint64_t len, uint64_t off, const char* path) 
   return ARK_OPT_OK;
 }
 
-int write_all(int fd, const void* buf, uint64_t len, const char* path) {
+// Positional write of [buf, buf + len) at file offset off, retrying short
+// writes.
+int pwrite_all(int fd, const void* buf, uint64_t len, uint64_t off, const char* path) {
   const uint8_t* p = (const uint8_t*)buf;
   while (len) {
-    const ssize_t k = ::write(fd, p, len > (1u << 30) ? (1u << 30) : len);
+    const ssize_t k = ::pwrite(fd, p, len > (1u << 30) ? (1u << 30) : len, (off_t)off);
     if (k < 0) {
       if (errno == EINTR) continue;
       return io_fail("write", path);
     }
     p += k;
+    off += (uint64_t)k;
     len -= (uint64_t)k;
   }
+  return ARK_OPT_OK;
+}
+
+// One staging chunk to or from the file, split over up to kIoThreads
+// threads (the single-threaded copy between the page cache and a pinned
+// buffer, not the GPU, bounds a checkpoint's save and load).
+constexpr int kIoThreads = 8;
+constexpr uint64_t kIoPiece = (uint64_t)4 << 20;  // at least 4 MiB per thread
+
+// memcpy split over up to kIoThreads threads (into a mapped file: the page
+// faults of the first touch run in parallel too).
+void parallel_copy(uint8_t* dst, const void* src, uint64_t len) {
+  unsigned hw = std::thread::hardware_concurrency();
+  int nt = (int)((len + kIoPiece - 1) / kIoPiece);
+  if (nt > kIoThreads) nt = kIoThreads;
+  if (hw && nt > (int)hw) nt = (int)hw;
+  if (nt <= 1) {
+    memcpy(dst, src, len);
+    return;
+  }
+  std::vector<std::thread> th;
+  const uint64_t piece = (len + nt - 1) / nt;
+  for (int t = 0; t < nt; ++t) {
+    const uint64_t a = (uint64_t)t * piece;
+    const uint64_t b = a + piece < len ? a + piece : len;
+    if (a >= b) break;
+    th.emplace_back([=] { memcpy(dst + a, (const uint8_t*)src + a, b - a); });
+  }
+  for (auto& x : th) x.join();
+}
+
+int parallel_io(bool write, int fd, void* buf, uint64_t len, uint64_t off, const char* path) {
+  unsigned hw = std::thread::hardware_concurrency();
+  int nt = (int)((len + kIoPiece - 1) / kIoPiece);
+  if (nt > kIoThreads) nt = kIoThreads;
+  if (hw && nt > (int)hw) nt = (int)hw;
+  if (nt <= 1)
+    return write ? pwrite_all(fd, buf, len, off, path) : read_exact(fd, buf, len, off, path);
+  std::vector<int> rc((size_t)nt, ARK_OPT_OK);
+  std::vector<std::string> msg((size_t)nt);
+  std::vector<std::thread> th;
+  const uint64_t piece = (len + nt - 1) / nt;
+  for (int t = 0; t < nt; ++t) {
+    const uint64_t a = (uint64_t)t * piece;
+    const uint64_t b = a + piece < len ? a + piece : len;
+    if (a >= b) break;
+    th.emplace_back([&, t, a, b] {
+      uint8_t* q = (uint8_t*)buf + a;
+      rc[t] = write ? pwrite_all(fd, q, b - a, off + a, path)
+                    : read_exact(fd, q, b - a, off + a, path);
+      if (rc[t]) msg[t] = ark::last_error();  // the message is per thread
+    });
+  }
+  for (auto& x : th) x.join();
+  for (int t = 0; t < nt; ++t)
+    if (rc[t]) return fail(rc[t], "%s", msg[t].c_str());
   return ARK_OPT_OK;
 }
 
@@ -750,8 +819,21 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
   } eg{ev};
   StreamSync sync{s};
   Fd f;
-  f.fd = ::open(path, O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+  f.fd = ::open(path, O_RDWR | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
   if (f.fd < 0) return io_fail("create", path);
+  // Preferred: reserve the whole file, map it, and copy each chunk into the
+  // mapping from several threads (writes to one file through write() are
+  // serialised by the file's lock).  The reservation makes a full disk fail
+  // here, with an error, instead of at a page fault.  Where reserving or
+  // mapping is not supported, fall back to pwrite.
+  FileMap map;
+  if (posix_fallocate(f.fd, 0, (off_t)L.total) == 0) {
+    void* m = mmap(nullptr, L.total, PROT_READ | PROT_WRITE, MAP_SHARED, f.fd, 0);
+    if (m != MAP_FAILED) {
+      map.p = (uint8_t*)m;
+      map.len = L.total;
+    }
+  }
   // chunk k: D2H into pin[k & 1]; while it runs, write chunk k - 1
   const uint64_t nchunks = (L.total + stage - 1) / stage;
   for (uint64_t k = 0; k <= nchunks; ++k) {
@@ -766,9 +848,14 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
       const uint64_t off = j * stage;
       const uint64_t len = L.total - off < stage ? L.total - off : stage;
       ARK_HIP(hipEventSynchronize(ev[j & 1]));
-      if ((rc = write_all(f.fd, pin[j & 1].p, len, path))) return rc;
+      if (map.p)
+        parallel_copy(map.p + off, pin[j & 1].p, len);
+      else if ((rc = parallel_io(true, f.fd, pin[j & 1].p, len, off, path)))
+        return rc;
     }
   }
+  if (map.p && munmap(map.p, map.len) != 0) return io_fail("unmap", path);
+  map.p = nullptr;
   const int fd = f.fd;
   f.fd = -1;
   if (::close(fd) != 0) return io_fail("close", path);
@@ -843,7 +930,7 @@ int ark_ckpt_load(const char* path, const ark_ckpt_record* records, int32_t n,
     const uint64_t off = k * stage;
     const uint64_t len = total - off < stage ? total - off : stage;
     if (k >= 2) ARK_HIP(hipEventSynchronize(ev[k & 1]));
-    if ((rc = read_exact(f.fd, pin[k & 1].p, len, off, path))) return rc;
+    if ((rc = parallel_io(false, f.fd, pin[k & 1].p, len, off, path))) return rc;
     ARK_HIP(hipMemcpyAsync((char*)img.p + off, pin[k & 1].p, len, hipMemcpyHostToDevice, s));
     ARK_HIP(hipEventRecord(ev[k & 1], s));
   }
