@@ -11,7 +11,8 @@ Prints one JSON line: value = achieved algorithmic HBM throughput of the
 whole step (24 B/param / step time) in GB/s; ms_per_step; a roofline object
 for the dominant kernel (the fused AdamW pass, 22 B/param, timed with HIP
 events on the stream it runs on); a cpu_baseline object (the C oracle on the
-host cores, a bounded sample of the same workload).
+host cores -- its 8-wide AVX2/F16C loops, bit-identical to the scalar
+restatement -- on a bounded sample of the same workload).
 """
 import argparse
 import json
@@ -135,6 +136,7 @@ def run_cpu_baseline(name, budget_s, threads):
     ts = H.host_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
     ref = oracle.Optimizer(ts, hparams(cfg, amp), nthreads=threads)
     n = sum(s.n for s in specs)
+    vec = oracle.set_vector(True)  # the 8-wide AVX2/F16C loops (same bits as the scalar form)
     ref.step(cfg.lr)  # warm (page in)
     done, t0 = 0, time.perf_counter()
     while True:
@@ -143,6 +145,7 @@ def run_cpu_baseline(name, budget_s, threads):
         el = time.perf_counter() - t0
         if el >= budget_s or done >= 1000:
             break
+    oracle.set_vector(False)
     s_step = el / done
     cpu = "unknown"
     try:
@@ -155,7 +158,8 @@ def run_cpu_baseline(name, budget_s, threads):
     return dict(value=round(BYTES_STEP * n / s_step / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port", ms_per_step=round(s_step * 1e3, 3),
                 sample=f"{done} full {name} steps ({n} params) in {el:.1f} s on {threads} "
-                       f"threads of {os.cpu_count()} ({cpu})")
+                       f"threads of {os.cpu_count()} ({cpu}), "
+                       f"{'8-wide AVX2/F16C' if vec else 'scalar'} loops")
 
 
 def traffic_from_profiles(name, kernel="adamw_kernel"):

@@ -54,6 +54,8 @@ def lib():
     L.ark_ref_compare_f32_to_f16_range.argtypes = [C.c_uint64, C.c_uint64, P, C.c_int,
                                                    C.POINTER(C.c_uint64)]
     L.ark_ref_compare_f32_to_f16_range.restype = C.c_int64
+    L.ark_ref_set_vector.argtypes = [C.c_int]
+    L.ark_ref_set_vector.restype = C.c_int
     L.ark_ref_grad_accumulate.argtypes = [P, P, C.c_uint64]
     L.ark_ref_grad_accumulate.restype = None
     L.ark_ref_embed_scatter.argtypes = [P, C.c_uint32, C.c_uint32, P, P, C.c_uint32]
@@ -126,6 +128,13 @@ def compare_f32_to_f16_range(lo, got, nthreads=8):
     bad = lib().ark_ref_compare_f32_to_f16_range(lo, lo + got.size, _ptr(got), nthreads,
                                                  C.byref(first))
     return bad, (None if first.value == 2 ** 64 - 1 else first.value)
+
+
+def set_vector(on):
+    """Run the optimizer step's loops 8-wide (AVX2/F16C) -- only to time the
+    CPU baseline; the checker uses the scalar restatement.  Returns the mode
+    in effect."""
+    return lib().ark_ref_set_vector(1 if on else 0)
 
 
 def grad_accumulate(dst, src):

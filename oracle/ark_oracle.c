@@ -353,6 +353,61 @@ static inline float grad_f32(const void *g, uint32_t dtype, uint64_t i) {
   return ((const float *)g)[i];
 }
 
+/* ------------------------------------------------------------------------ */
+/* Optional 8-wide AVX2/F16C form of the two hot loops, used only to time   */
+/* the CPU baseline.  Off by default: the checker runs the scalar           */
+/* restatement.  Every operation is the same IEEE binary32 operation (F16C  */
+/* conversions equal the software ones bit for bit, NaNs included; vsqrtps  */
+/* and vdivps are correctly rounded; vfmadd is one fused rounding like      */
+/* fmaf), so both forms give identical bits -- a CPU test checks it.        */
+/* ------------------------------------------------------------------------ */
+
+static int g_vector = 0;
+
+int ark_ref_set_vector(int on) {
+#if defined(__AVX2__) && defined(__F16C__) && defined(__FMA__)
+  g_vector = on ? 1 : 0;
+  return g_vector;
+#else
+  (void)on;
+  return 0;
+#endif
+}
+
+#if defined(__AVX2__) && defined(__F16C__) && defined(__FMA__)
+/* Squares of 8 unscaled fp16 gradients into q[0..8) (f64, exact) and the
+ * non-finite flag of the 8. */
+static inline int sq8_f16(const uint16_t *g, float inv_t, double *q) {
+  __m128i h = _mm_loadu_si128((const __m128i *)g);
+  __m128i ex = _mm_and_si128(h, _mm_set1_epi16(0x7C00));
+  int bad = _mm_movemask_epi8(_mm_cmpeq_epi16(ex, _mm_set1_epi16(0x7C00))) != 0;
+  __m256 f = _mm256_mul_ps(_mm256_cvtph_ps(h), _mm256_set1_ps(inv_t));
+  __m256d lo = _mm256_cvtps_pd(_mm256_castps256_ps128(f));
+  __m256d hi = _mm256_cvtps_pd(_mm256_extractf128_ps(f, 1));
+  _mm256_storeu_pd(q, _mm256_mul_pd(lo, lo));
+  _mm256_storeu_pd(q + 4, _mm256_mul_pd(hi, hi));
+  return bad;
+}
+
+/* 8 elements of adam_elem with g already unscaled and clipped. */
+static inline void adam8(uint16_t *w16, __m256 g, float *m, float *v, const ark_ref_scalars *s,
+                         float beta1, float beta2, float eps) {
+  __m256 w = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)w16));
+  __m256 mm = _mm256_mul_ps(_mm256_loadu_ps(m), _mm256_set1_ps(beta1));
+  mm = _mm256_fmadd_ps(_mm256_set1_ps(s->c1), g, mm);
+  __m256 vv = _mm256_mul_ps(_mm256_loadu_ps(v), _mm256_set1_ps(beta2));
+  __m256 gg = _mm256_mul_ps(g, g);
+  vv = _mm256_fmadd_ps(_mm256_set1_ps(s->c2), gg, vv);
+  __m256 d = _mm256_add_ps(_mm256_sqrt_ps(vv), _mm256_set1_ps(eps));
+  __m256 u = _mm256_mul_ps(_mm256_div_ps(mm, d), _mm256_set1_ps(s->lr_eff));
+  w = _mm256_sub_ps(_mm256_mul_ps(w, _mm256_set1_ps(s->decay)), u);
+  _mm256_storeu_ps(m, mm);
+  _mm256_storeu_ps(v, vv);
+  _mm_storeu_si128((__m128i *)w16,
+                   _mm256_cvtps_ph(w, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+}
+#endif
+
 typedef struct {
   const ark_opt_tensor *tab;
   int32_t nt;
@@ -376,7 +431,13 @@ static void sumsq_worker(void *p, int tid, int nth) {
     float inv_t = (T->flags & ARK_OPT_TENSOR_NO_UNSCALE) ? 1.0f : c->inv;
     uint64_t st = c->seg_start[s];
     uint64_t len = T->n - st < SEG ? T->n - st : SEG;
-    for (uint64_t j = 0; j < len; ++j) {
+    uint64_t j0 = 0;
+#if defined(__AVX2__) && defined(__F16C__) && defined(__FMA__)
+    if (g_vector && c->dtype == ARK_OPT_GRAD_F16)
+      for (; j0 + 8 <= len; j0 += 8)
+        bad |= sq8_f16((const uint16_t *)T->g + st + j0, inv_t, buf + j0);
+#endif
+    for (uint64_t j = j0; j < len; ++j) {
       bad |= grad_nonfinite(T->g, c->dtype, st + j);
       float gu = grad_f32(T->g, c->dtype, st + j) * inv_t; /* vDSP_vsmul */
       buf[j] = (double)gu * (double)gu;                     /* exact */
@@ -467,7 +528,22 @@ static void upd_worker(void *p, int tid, int nth) {
     ark_ref_prologue(c->lr, c->hp->beta1, c->hp->beta2, T->weight_decay, c->t,
                      &s);
     float inv_t = (T->flags & ARK_OPT_TENSOR_NO_UNSCALE) ? 1.0f : c->inv;
-    for (uint64_t e = s0 - a; e < s1 - a; ++e) {
+    uint64_t e0 = s0 - a;
+#if defined(__AVX2__) && defined(__F16C__) && defined(__FMA__)
+    if (g_vector) {
+      const __m256 vinv = _mm256_set1_ps(inv_t), vcoef = _mm256_set1_ps(c->coef);
+      for (; e0 + 8 <= s1 - a; e0 += 8) {
+        __m256 g = c->hp->grad_dtype == ARK_OPT_GRAD_F16
+                       ? _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)((const uint16_t *)T->g + e0)))
+                       : _mm256_loadu_ps((const float *)T->g + e0);
+        g = _mm256_mul_ps(g, vinv);
+        if (c->clipped) g = _mm256_mul_ps(g, vcoef);
+        adam8(T->w + e0, g, T->m + e0, T->v + e0, &s, c->hp->beta1, c->hp->beta2,
+              c->hp->eps);
+      }
+    }
+#endif
+    for (uint64_t e = e0; e < s1 - a; ++e) {
       float g = grad_f32(T->g, c->hp->grad_dtype, e) * inv_t; /* training.rs:308 */
       if (c->clipped) g = g * c->coef; /* optimizer.rs:151-165 */
       T->w[e] = adam_elem(T->w[e], g, &T->m[e], &T->v[e], &s, c->hp->beta1,

@@ -60,6 +60,11 @@ typedef struct ark_ref_scalars {
 void ark_ref_prologue(float lr, float beta1, float beta2, float wd, uint32_t t,
                       ark_ref_scalars *out);
 
+/* 1: the step's two loops (sum of squares, update) run 8-wide with AVX2/F16C
+ * (for timing the CPU baseline; identical bits); 0 (default): the scalar
+ * restatement.  Returns the mode in effect (0 without AVX2/F16C/FMA). */
+int ark_ref_set_vector(int on);
+
 /* Exact transliteration of ark_asm_adam_step_f16 (opti.s:192-360). */
 void ark_ref_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
                            uint64_t n, float lr, float beta1, float beta2,
