@@ -65,6 +65,11 @@ def run_gpu(name, steps, warmup):
     cfg = AdamConfig(**HP)
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
+    # everything on one non-default stream, so the step can also be captured
+    # in a HIP graph below
+    stream = torch.cuda.Stream()
+    stream_ctx = torch.cuda.stream(stream)
+    stream_ctx.__enter__()
     ps = H.gpu_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
     opt = Optimizer(cfg, ps, amp)
     torch.cuda.synchronize()
@@ -90,6 +95,21 @@ def run_gpu(name, steps, warmup):
     torch.cuda.synchronize()
     tm = opt.get_timing()
     opt.set_timing(False)
+
+    # the same step captured once in a HIP graph and replayed K times
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        opt.step_all(cfg.lr)
+    for _ in range(min(warmup, 5)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+
     _, last = opt.step_all(cfg.lr, info=True)
     n = ps.n_params
     res = dict(
@@ -97,9 +117,10 @@ def run_gpu(name, steps, warmup):
         ms_adamw=tm.ms_adamw / tm.steps, ms_norm=tm.ms_norm / tm.steps,
         ms_finalize=tm.ms_finalize / tm.steps, ms_step_events=tm.ms_step / tm.steps,
         clipped=int(last.clipped), applied=int(last.applied), t=int(last.state.t),
-        grad_norm=float(last.grad_norm),
+        grad_norm=float(last.grad_norm), graph_ms=graph_ms,
     )
     opt.close()
+    stream_ctx.__exit__(None, None, None)
     del ps
     torch.cuda.empty_cache()
     return res
@@ -472,6 +493,7 @@ def main():
             "loss_scale": WORKLOADS[a.workload]["loss_scale"],
             "clipped": r["clipped"],
             "grad_norm": r["grad_norm"],
+            "hip_graph_ms_per_step": round(r["graph_ms"], 4),
         },
         "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4),
         "kernels_ms": {"sumsq": round(r["ms_norm"], 4), "finalize": round(r["ms_finalize"], 4),
