@@ -132,3 +132,7 @@ class CkptInfo(C.Structure):
 # include/ark_grad.h
 class GradSpan(C.Structure):
     _fields_ = [("dst", C.c_void_p), ("src", C.c_void_p), ("n", C.c_uint64)]
+
+
+# every struct whose size ark_opt_struct_sizes reports, in its order
+ALL_STRUCTS = STRUCTS + (CodecSpan, CkptRecord, CkptInfo, GradSpan)

@@ -94,9 +94,11 @@ def lib():
     _declare(L)
     if L.ark_opt_abi_version() != _abi.ABI_VERSION:
         raise ImportError("libark_opt ABI version mismatch")
-    sizes = (C.c_size_t * 5)()
-    L.ark_opt_struct_sizes(sizes, 5)
-    for s, st in zip(sizes, _abi.STRUCTS):
+    k = len(_abi.ALL_STRUCTS)
+    sizes = (C.c_size_t * k)()
+    if L.ark_opt_struct_sizes(sizes, k) != k:
+        raise ImportError("libark_opt reports fewer struct sizes than the bindings know")
+    for s, st in zip(sizes, _abi.ALL_STRUCTS):
         if s != C.sizeof(st):
             raise ImportError(f"struct {st.__name__}: C size {s} != ctypes size {C.sizeof(st)}")
     _lib = L

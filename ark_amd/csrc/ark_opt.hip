@@ -10,7 +10,10 @@
 #include <string>
 #include <vector>
 
+#include "ark_ckpt.h"
+#include "ark_codec.h"
 #include "ark_common.hpp"
+#include "ark_grad.h"
 #include "ark_opt_kernels.hpp"
 
 using ark::SegDesc;
@@ -113,11 +116,11 @@ int ark_opt_abi_version(void) { return ARK_OPT_ABI_VERSION; }
 const char* ark_opt_last_error(void) { return ark::last_error(); }
 
 int ark_opt_struct_sizes(size_t* out, int n) {
-  const size_t s[5] = {sizeof(ark_opt_tensor), sizeof(ark_opt_hparams),
-                       sizeof(ark_opt_state), sizeof(ark_opt_step_info),
-                       sizeof(ark_opt_timing)};
+  const size_t s[9] = {sizeof(ark_opt_tensor),  sizeof(ark_opt_hparams), sizeof(ark_opt_state),
+                       sizeof(ark_opt_step_info), sizeof(ark_opt_timing), sizeof(ark_codec_span),
+                       sizeof(ark_ckpt_record), sizeof(ark_ckpt_info),  sizeof(ark_grad_span)};
   if (!out || n < 0) return fail(ARK_OPT_EINVAL, "out is NULL");
-  int k = n < 5 ? n : 5;
+  int k = n < 9 ? n : 9;
   for (int i = 0; i < k; ++i) out[i] = s[i];
   return k;
 }

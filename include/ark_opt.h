@@ -142,8 +142,9 @@ int ark_opt_abi_version(void);
 const char *ark_opt_last_error(void);
 
 /* sizeof of each public struct, in the order tensor, hparams, state,
- * step_info, timing; lets a binding check its layouts.  Returns the count
- * written (at most n). */
+ * step_info, timing, then ark_codec_span, ark_ckpt_record, ark_ckpt_info,
+ * ark_grad_span (include/ark_codec.h, ark_ckpt.h, ark_grad.h); lets a
+ * binding check its layouts.  Returns the count written (at most n). */
 int ark_opt_struct_sizes(size_t *out, int n);
 
 /* Defaults: AdamConfig::default (optimizer.rs:54-66: beta1 0.9, beta2 0.999,

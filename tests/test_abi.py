@@ -31,6 +31,11 @@ def test_struct_layouts_match():
     sizes = (C.c_size_t * 5)()
     assert L.ark_opt_struct_sizes(sizes, 5) == 5
     assert list(sizes) == [C.sizeof(s) for s in _abi.STRUCTS]
+    k = len(_abi.ALL_STRUCTS)
+    sizes = (C.c_size_t * (k + 3))()
+    assert L.ark_opt_struct_sizes(sizes, k + 3) == k  # no more than it knows
+    assert list(sizes)[:k] == [C.sizeof(s) for s in _abi.ALL_STRUCTS]
+    assert [C.sizeof(s) for s in _abi.ALL_STRUCTS[5:]] == [24, 24, 48, 24]
     assert L.ark_opt_abi_version() == _abi.ABI_VERSION
     assert L.ark_opt_struct_sizes(None, 5) == _abi.EINVAL
 
