@@ -6,7 +6,7 @@
 // block starts at an arbitrary byte offset.  The kernels work in 16-byte
 // chunks of the aligned side and shift the other side into place:
 //
-//   pack_kernel   one block per <= 16 KiB of image inside one tensor's data
+//   pack_kernel   one block per <= 4 KiB of image inside one tensor's data
 //                 (the block finds its tensor in a per-tensor table);
 //                 a lane owns aligned 16-byte image chunks, loads the two
 //                 aligned 16-byte source blocks that cover the chunk and
@@ -15,8 +15,9 @@
 //                 edge, or whose second block would pass the end of the
 //                 source, go byte by byte.
 //   header_kernel the file header, tensor headers and trailer, byte stores.
-//   unpack_kernel one block per 4096 elements of one tensor (found the same
-//                 way, both file types in one launch); a lane takes
+//   unpack_kernel one block per 2048 (fp16) or 1024 (fp32) elements of one
+//                 tensor (found the same way, both file types in one
+//                 launch); a lane takes
 //                 16-byte units of the image (8 fp16 or 4 fp32 elements),
 //                 shifts them out of two aligned loads, converts to the
 //                 destination type and stores aligned.
@@ -49,9 +50,12 @@ constexpr uint64_t kRecHeaderV4 = 16;   // u64 n + u64 type (io.rs:460-461, :467
 constexpr uint64_t kTrailerBytes = 40;  // u32 magic + u32 version + ark_opt_state
 constexpr uint32_t kTrailerVersion = 1;
 constexpr int kThreads = 256;
-constexpr uint32_t kPackSegBytes = 16384;             // image bytes per pack block
-constexpr int kPackChunks = kPackSegBytes / (16 * kThreads);  // 4 per lane
-constexpr uint32_t kUnpackSeg = 4096;                 // elements per unpack block
+// One 16-byte chunk or unit per lane per block (many small blocks stream
+// faster on MI355X than a few with several accesses per lane).
+constexpr uint32_t kPackSegBytes = 16 * kThreads;     // image bytes per pack block
+constexpr int kPackChunks = kPackSegBytes / (16 * kThreads);  // 1 per lane
+// elements per unpack block: one 16-byte unit of the file type per lane
+constexpr uint32_t unpack_seg(uint32_t ftype) { return (ftype == ARK_CKPT_F16 ? 8u : 4u) * kThreads; }
 constexpr size_t kStageBytes = (size_t)64 << 20;      // per pinned staging buffer
 static_assert(sizeof(ark_opt_state) == 32, "trailer holds a 32-byte state");
 
@@ -241,11 +245,12 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
                                              const uint8_t* __restrict__ img, uint64_t img_bytes) {
   constexpr uint32_t kFs = FT == ARK_CKPT_F16 ? 2u : 4u;  // file element bytes
   constexpr uint32_t kU = 16u / kFs;                       // elements per unit
-  constexpr int kUnits = (int)(kUnpackSeg / kU / kThreads);  // 2 or 4 per lane
+  constexpr uint32_t kSegN = unpack_seg(FT);
+  constexpr int kUnits = (int)(kSegN / kU / kThreads);     // 1 per lane
   const uint32_t ds = s.dtype == ARK_CKPT_F16 ? 2u : 4u;
   const uint64_t src_off = s.src_off + e_begin * kFs;
   const uint32_t sh = (uint32_t)(src_off & 15u);
-  const uint64_t n = s.n - e_begin < kUnpackSeg ? s.n - e_begin : kUnpackSeg;
+  const uint64_t n = s.n - e_begin < kSegN ? s.n - e_begin : kSegN;
   uint8_t* dst0 = (uint8_t*)s.dst + e_begin * ds;
 #pragma unroll
   for (int k = 0; k < kUnits; ++k) {
@@ -271,7 +276,8 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
   }
 }
 
-// Block j of a tensor converts its elements [j*4096, (j+1)*4096).
+// Block j of a tensor converts its elements [j*S, (j+1)*S), S = 2048 for an
+// F16 file tensor and 1024 for F32 (one 16-byte unit per lane).
 __global__ __launch_bounds__(kThreads) void unpack_kernel(const UnpackRec* __restrict__ recs,
                                                           const uint32_t* __restrict__ start,
                                                           uint32_t nrec,
@@ -279,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const UnpackRec* __res
                                                           uint64_t img_bytes) {
   const uint32_t r = find_rec(start, nrec, blockIdx.x);
   const UnpackRec s = recs[r];
-  const uint64_t e_begin = (uint64_t)(blockIdx.x - start[r]) * kUnpackSeg;
+  const uint64_t e_begin = (uint64_t)(blockIdx.x - start[r]) * unpack_seg(s.ftype);
   if (s.ftype == ARK_CKPT_F16)
     unpack_block<ARK_CKPT_F16>(s, e_begin, img, img_bytes);
   else
@@ -507,7 +513,7 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
     u.ftype = (uint8_t)ftype[i];
     u.dst_vec = ((uintptr_t)r[i].data & 15u) == 0;
     start[i] = (uint32_t)blocks;
-    blocks += (r[i].n + kUnpackSeg - 1) / kUnpackSeg;
+    blocks += (r[i].n + unpack_seg(ftype[i]) - 1) / unpack_seg(ftype[i]);
     if (blocks > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "checkpoint too large");
   }
   start[n] = (uint32_t)blocks;

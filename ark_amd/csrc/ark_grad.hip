@@ -4,8 +4,9 @@
 //   grad_flat / grad_batch  dst += src in fp32: 12 bytes per element (two
 //       reads, one write), HBM bound.  Same shape as the weight codec: a lane
 //       takes 4 consecutive elements per access, consecutive lanes
-//       consecutive quads; the batch form runs one 4096-element segment per
-//       256-lane block from a descriptor table, all tensors in one launch.
+//       consecutive quads; the batch form runs each 4096-element segment of
+//       a descriptor table as sixteen one-wave blocks, all tensors in one
+//       launch.
 //   embed scatter  the loop of bridge.m:922-928 adds row i of dx0 into the
 //       embedding row of token i, in increasing i.  Atomics would add in an
 //       arbitrary order and change the fp32 sums, so instead:
@@ -35,8 +36,9 @@ using ark::fail;
 constexpr int kThreads = 256;
 constexpr int kPerLane = 4;
 constexpr uint32_t kSeg = 4096;
-constexpr int kQuadsPerLane = kSeg / (kThreads * kPerLane);  // 4
-constexpr int kTileCols = 64 * kPerLane;                      // run_kernel: 256 columns per wave
+constexpr int kWave = 64;
+constexpr uint32_t kBlocksPerSeg = kSeg / (kWave * kPerLane);  // 16
+constexpr int kTileCols = kWave * kPerLane;                   // run_kernel: 256 columns per wave
 constexpr int kRowBatch = 32;                                 // dx0 rows in flight per wave
 
 struct GradSeg {
@@ -77,24 +79,18 @@ __global__ __launch_bounds__(kThreads) void grad_flat(float* __restrict__ dst,
   }
 }
 
-__global__ __launch_bounds__(kThreads) void grad_batch(const GradSeg* __restrict__ segs) {
-  const GradSeg d = segs[blockIdx.x];
-  if (d.vec && d.n == kSeg) {
-#pragma unroll
-    for (int k = 0; k < kQuadsPerLane; ++k) {
-      const uint32_t e0 = ((uint32_t)k * kThreads + threadIdx.x) * kPerLane;
-      add4(d.dst + e0, d.src + e0);
-    }
-    return;
-  }
-  for (int k = 0; k < kQuadsPerLane; ++k) {
-    const uint32_t e0 = ((uint32_t)k * kThreads + threadIdx.x) * kPerLane;
-    if (d.vec && e0 + kPerLane <= d.n) {
-      add4(d.dst + e0, d.src + e0);
-    } else {
-      for (int j = 0; j < kPerLane; ++j)
-        if (e0 + j < d.n) add1(d.dst + e0 + j, d.src + e0 + j);
-    }
+// Sixteen one-wave blocks per segment, one quad per lane: block b adds
+// elements [(b % 16) * 256 + 4l, +4) of segment b / 16 (the shape the sweep
+// measured fastest for two read streams and one write stream).
+__global__ __launch_bounds__(kWave) void grad_batch(const GradSeg* __restrict__ segs) {
+  const GradSeg d = segs[blockIdx.x / kBlocksPerSeg];
+  const uint32_t e0 = ((blockIdx.x % kBlocksPerSeg) * kWave + threadIdx.x) * kPerLane;
+  if (e0 >= d.n) return;
+  if (d.vec && e0 + kPerLane <= d.n) {
+    add4(d.dst + e0, d.src + e0);
+  } else {
+    for (int j = 0; j < kPerLane; ++j)
+      if (e0 + j < d.n) add1(d.dst + e0 + j, d.src + e0 + j);
   }
 }
 
@@ -238,7 +234,8 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      if (segs.size() > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "too many elements");
+      if (segs.size() > 0x7FFFFFFFu / kBlocksPerSeg)
+        return fail(ARK_OPT_EINVAL, "too many elements");
     }
   }
   ark_grad_plan* p = new ark_grad_plan();
@@ -264,7 +261,8 @@ int ark_grad_plan_run(ark_grad_plan* p) {
   if (p->nseg == 0) return ARK_OPT_OK;
   ark::DeviceGuard g(p->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
-  hipLaunchKernelGGL(grad_batch, dim3(p->nseg), dim3(kThreads), 0, p->stream, p->d_segs);
+  hipLaunchKernelGGL(grad_batch, dim3(p->nseg * kBlocksPerSeg), dim3(kWave), 0, p->stream,
+                     p->d_segs);
   ARK_HIP(hipGetLastError());
   return ARK_OPT_OK;
 }
