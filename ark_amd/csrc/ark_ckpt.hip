@@ -833,7 +833,9 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
   // here, with an error, instead of at a page fault.  Where reserving or
   // mapping is not supported, fall back to pwrite.
   FileMap map;
-  if (posix_fallocate(f.fd, 0, (off_t)L.total) == 0) {
+  // fallocate (not posix_fallocate, which falls back to writing zeros where
+  // the file system cannot reserve): unsupported means pwrite instead.
+  if (fallocate(f.fd, 0, 0, (off_t)L.total) == 0) {
     void* m = mmap(nullptr, L.total, PROT_READ | PROT_WRITE, MAP_SHARED, f.fd, 0);
     if (m != MAP_FAILED) {
       map.p = (uint8_t*)m;
