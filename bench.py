@@ -54,22 +54,26 @@ def sigmas_for(name, specs):
 
 def run_gpu(name, steps, warmup):
     import torch
+    torch.cuda.set_device(0)
+    # everything on one non-default stream, so the step can also be captured
+    # in a HIP graph
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        return _run_gpu(name, steps, warmup, stream)
+
+
+def _run_gpu(name, steps, warmup, stream):
+    import torch
     from ark_amd.eko import config_tensors
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
     from oracle import harness as H
 
-    torch.cuda.set_device(0)
     specs = config_tensors(name)
     w = WORKLOADS[name]
     sig = sigmas_for(name, specs)
     cfg = AdamConfig(**HP)
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
-    # everything on one non-default stream, so the step can also be captured
-    # in a HIP graph below
-    stream = torch.cuda.Stream()
-    stream_ctx = torch.cuda.stream(stream)
-    stream_ctx.__enter__()
     ps = H.gpu_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
     opt = Optimizer(cfg, ps, amp)
     torch.cuda.synchronize()
@@ -120,7 +124,6 @@ def run_gpu(name, steps, warmup):
         grad_norm=float(last.grad_norm), graph_ms=graph_ms,
     )
     opt.close()
-    stream_ctx.__exit__(None, None, None)
     del ps
     torch.cuda.empty_cache()
     return res

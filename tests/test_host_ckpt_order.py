@@ -1,0 +1,66 @@
+"""Host logic of the checkpoint and codec mirrors, on the CPU: the V4 tensor
+order built from a ParamSet (Trainer::guardar_checkpoint, training.rs:536-604,
+into CheckpointV3::save_fp16's order, io.rs:473-494); the oracle's writer fed
+in that order reproduces the regrouping the reference's loader expects."""
+import numpy as np
+
+from ark_amd import ckpt
+from ark_amd.eko import EkoConfig
+from oracle import ckpt as K
+
+
+def _cpu_params(cfg):
+    from ark_amd.optimizer import ParamSet
+    return ParamSet(cfg.tensors(), weight_decay=0.1, device="cpu")
+
+
+def _names(ps, tensors):
+    """Map each tensor view back to (spec name, kind) by its storage offset."""
+    out = []
+    for t in tensors:
+        for arena, kind in ((ps.w_arena, "w"), (ps.m_arena, "m"), (ps.v_arena, "v")):
+            if t.untyped_storage().data_ptr() == arena.untyped_storage().data_ptr():
+                off = t.storage_offset()
+                i = ps.offsets.index(off)
+                out.append((ps.specs[i].name, kind))
+    return out
+
+
+def test_param_tensors_follow_save_fp16_order():
+    cfg = EkoConfig(n_layers=2, d_model=8, hidden=12, vocab=10)
+    ps = _cpu_params(cfg)
+    got = _names(ps, ckpt.param_tensors(ps))
+    lw = ["wq", "wk", "wv", "wo", "w1", "w2", "w3", "g1", "g2"]
+    want = [("embed", "w"), ("embed", "m"), ("embed", "v")]
+    for l in range(2):
+        want += [(f"l{l}.{k}", "w") for k in lw]
+        want += [(f"l{l}.{k}", "m") for k in lw]
+        want += [(f"l{l}.{k}", "v") for k in lw]
+    want += [("gamma_final", "w"), ("gamma_final", "m"), ("gamma_final", "v")]
+    assert got == want
+    assert len(got) == 3 + 27 * 2 + 3
+    # weights-only (V2) order: embed, then each layer's 9
+    w_only = _names(ps, ckpt.param_tensors(ps, with_moments=False))
+    assert w_only == [("embed", "w")] + [(f"l{l}.{k}", "w") for l in range(2) for k in lw]
+
+
+def test_oracle_loader_regroups_that_order():
+    """The file the oracle writes in param_tensors order regroups into
+    pesos = [embed, layers' 9, gamma_final] exactly as io.rs:569-586 does."""
+    cfg = EkoConfig(n_layers=2, d_model=8, hidden=12, vocab=10)
+    ps = _cpu_params(cfg)
+    rng = np.random.default_rng(0)
+    host = []
+    for t in ckpt.param_tensors(ps):
+        a = rng.standard_normal(t.numel()).astype(np.float32)
+        host.append(a.astype(np.float16).view(np.uint16) if t.element_size() == 2 else a)
+    buf = K.write_v4(5, 4, host)
+    r = K.load(buf)
+    names = [n for n, k in _names(ps, ckpt.param_tensors(ps)) if k == "w"]
+    assert len(r["pesos"]) == len(names) == 1 + 18 + 1
+    # pesos[i] is the i-th weight in file order, widened to fp32
+    ws = [h for h, (n, k) in zip(host, _names(ps, ckpt.param_tensors(ps))) if k == "w"]
+    for a, b in zip(r["pesos"], ws):
+        np.testing.assert_array_equal(a.view(np.uint32),
+                                      b.astype(np.uint16).view(np.float16).astype(np.float32)
+                                      .view(np.uint32))
