@@ -114,3 +114,27 @@ def test_headers_cite_reference_interfaces():
     for cite in ("opti.s:189-193", "optimizer.rs:171-228", "training.rs:289-326",
                  "training.rs:228-241", "optimizer.rs:237-313"):
         assert cite in text
+
+
+def test_next_rows_reject_bad_arguments_before_device_calls():
+    """The codec, gradient and checkpoint entry points refuse NULL buffers,
+    misalignment and unknown enums with EINVAL and a message, before any
+    HIP call."""
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    assert L.ark_hip_dequant_f16_to_f32(None, None, 0, None) == 0  # n == 0 is a no-op
+    assert L.ark_hip_dequant_f16_to_f32(None, None, 8, None) == _abi.EINVAL and "NULL" in msg()
+    assert L.ark_hip_quant_f32_to_f16(2, 16, 8, None) == _abi.EINVAL and "aligned" in msg()
+    h = C.c_void_p()
+    assert L.ark_codec_plan_create(None, 1, 0, None, C.byref(h)) == _abi.EINVAL
+    assert L.ark_codec_plan_create(None, 0, 7, None, C.byref(h)) == _abi.EINVAL and "direction" in msg()
+    assert L.ark_grad_accumulate(None, None, 4, None) == _abi.EINVAL
+    assert L.ark_grad_accumulate(6, 8, 4, None) == _abi.EINVAL and "aligned" in msg()
+    assert L.ark_grad_embed_scatter(None, 0, 4, None, None, 3, None) == _abi.EINVAL and "vocab" in msg()
+    assert L.ark_grad_embed_scatter(None, 10, 4, None, None, 0, None) == 0  # empty batch
+    recs = (_abi.CkptRecord * 1)()
+    recs[0] = _abi.CkptRecord(0, 4, 9, 0)
+    out = C.c_uint64()
+    assert L.ark_ckpt_v4_image_bytes(recs, 1, 0, C.byref(out)) == _abi.EINVAL and "dtype" in msg()
+    assert L.ark_ckpt_save_v4(None, 0, 0, recs, 1, None, None) == _abi.EINVAL
+    assert L.ark_ckpt_probe(None, None, None, None, 0) == _abi.EINVAL
