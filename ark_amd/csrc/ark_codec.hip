@@ -7,8 +7,8 @@
 // fall back to per-element accesses.
 //
 // The batch kernel takes 4096-element segments from a descriptor table
-// (source and destination already offset to the segment), four 256-lane
-// blocks per segment, so a whole model's tensors convert in a single launch.
+// (source and destination already offset to the segment), several blocks per
+// segment, so a whole model's tensors convert in a single launch.
 #include <string.h>
 
 #include <vector>
@@ -21,11 +21,23 @@ namespace {
 
 using namespace ark::dev;
 
-constexpr int kThreads = 256;
 constexpr int kPerLane = 4;      // elements per access: 8 B of fp16, 16 B of fp32
-constexpr uint32_t kSeg = 4096;  // batch kernel: elements per block
-constexpr uint32_t kBlocksPerSeg = kSeg / (kThreads * kPerLane);  // 4
-static_assert(kBlocksPerSeg * kThreads * kPerLane == kSeg, "segment shape");
+constexpr int kQuads = 2;        // accesses per lane, kLanes * 4 elements apart
+constexpr uint32_t kSeg = 4096;  // batch kernel: elements per segment
+
+// Lanes per block by direction.  Measured on MI355X over the EKO-237M weight
+// set with the Infinity Cache flushed before each launch: two quads per lane
+// with 64-lane blocks dequantise at 6.45 TB/s and with 256-lane blocks
+// quantise at 6.69 TB/s, where one quad per lane in 256-lane blocks reaches
+// 5.5 and 6.1 TB/s, and four or more quads per lane fall back below 6.2.
+template <uint32_t DIR>
+struct Shape {
+  static constexpr uint32_t kLanes = DIR == ARK_CODEC_F16_TO_F32 ? 64u : 256u;
+  static constexpr uint32_t kSpan = kLanes * kPerLane * kQuads;  // elements per block
+  static constexpr uint32_t kBlocksPerSeg = kSeg / kSpan;
+  static_assert(kBlocksPerSeg * kSpan == kSeg, "segment shape");
+};
+constexpr uint32_t kMaxBlocksPerSeg = Shape<ARK_CODEC_F16_TO_F32>::kBlocksPerSeg;  // 8
 
 struct CodecSeg {
   const void* src;
@@ -73,16 +85,17 @@ constexpr uint32_t src_size() { return DIR == ARK_CODEC_F16_TO_F32 ? 2u : 4u; }
 template <uint32_t DIR>
 constexpr uint32_t dst_size() { return DIR == ARK_CODEC_F16_TO_F32 ? 4u : 2u; }
 
-// One flat range; grid-stride over quads (one pass for every size the grid
-// cap allows, 2^30 elements).
+// The block's span [b0, b0 + kSpan) of a range of n elements: lane l converts
+// the quads at b0 + 4l and b0 + 4l + 4 * kLanes (each access instruction of a
+// wave covers one contiguous stretch).  vec: both pointers 16-byte aligned.
 template <uint32_t DIR>
-__global__ __launch_bounds__(kThreads) void codec_flat(const void* __restrict__ src,
-                                                       void* __restrict__ dst, uint64_t n,
-                                                       uint32_t vec) {
-  const uint64_t nquad = (n + kPerLane - 1) / kPerLane;
-  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-  for (uint64_t q = (uint64_t)blockIdx.x * kThreads + threadIdx.x; q < nquad; q += stride) {
-    const uint64_t e0 = q * kPerLane;
+__device__ __forceinline__ void convert_span(const void* src, void* dst, uint64_t b0, uint64_t n,
+                                             uint32_t vec) {
+  constexpr uint32_t L = Shape<DIR>::kLanes;
+#pragma unroll
+  for (int u = 0; u < kQuads; ++u) {
+    const uint64_t e0 = b0 + (uint64_t)(u * L + threadIdx.x) * kPerLane;
+    if (e0 >= n) return;  // the next quad lies further on
     if (vec && e0 + kPerLane <= n) {
       conv4<DIR>((const char*)src + e0 * src_size<DIR>(), (char*)dst + e0 * dst_size<DIR>());
     } else {
@@ -92,21 +105,25 @@ __global__ __launch_bounds__(kThreads) void codec_flat(const void* __restrict__ 
   }
 }
 
-// Four 256-lane blocks per segment, one quad per lane: block b converts
-// elements [(b % 4) * 1024 + 4t, +4) of segment b / 4.  (Measured on MI355X:
-// one access per lane over many blocks streams 15-20 % faster than four
-// accesses per lane over a quarter of the blocks.)
+// One flat range; blocks take consecutive spans, grid-stride (one pass for
+// every size up to the grid cap times the span).
 template <uint32_t DIR>
-__global__ __launch_bounds__(kThreads) void codec_batch(const CodecSeg* __restrict__ segs) {
-  const CodecSeg d = segs[blockIdx.x / kBlocksPerSeg];
-  const uint32_t e0 = ((blockIdx.x % kBlocksPerSeg) * kThreads + threadIdx.x) * kPerLane;
-  if (e0 >= d.n) return;
-  if (d.vec && e0 + kPerLane <= d.n) {
-    conv4<DIR>((const char*)d.src + e0 * src_size<DIR>(), (char*)d.dst + e0 * dst_size<DIR>());
-  } else {
-    for (int j = 0; j < kPerLane; ++j)
-      if (e0 + j < d.n) conv1<DIR>(d.src, d.dst, e0 + j);
-  }
+__global__ __launch_bounds__(Shape<DIR>::kLanes) void codec_flat(const void* __restrict__ src,
+                                                                 void* __restrict__ dst,
+                                                                 uint64_t n, uint32_t vec) {
+  constexpr uint64_t S = Shape<DIR>::kSpan;
+  for (uint64_t b0 = (uint64_t)blockIdx.x * S; b0 < n; b0 += (uint64_t)gridDim.x * S)
+    convert_span<DIR>(src, dst, b0, n, vec);
+}
+
+// Shape<DIR>::kBlocksPerSeg blocks per segment: block b converts the span
+// (b % kBlocksPerSeg) of segment b / kBlocksPerSeg.
+template <uint32_t DIR>
+__global__ __launch_bounds__(Shape<DIR>::kLanes) void codec_batch(
+    const CodecSeg* __restrict__ segs) {
+  constexpr uint32_t B = Shape<DIR>::kBlocksPerSeg;
+  const CodecSeg d = segs[blockIdx.x / B];
+  convert_span<DIR>(d.src, d.dst, (uint64_t)(blockIdx.x % B) * Shape<DIR>::kSpan, d.n, d.vec);
 }
 
 constexpr uint64_t kMaxFlatBlocks = 1u << 20;
@@ -128,9 +145,9 @@ int run_flat(const void* src, void* dst, uint64_t n, void* stream) {
   if ((rc = ark::check_buffer(dst, db, "dst", 0))) return rc;
   if (overlaps(src, sb, dst, db)) return ark::fail(ARK_OPT_EINVAL, "src and dst overlap");
   const uint32_t vec = ((((uintptr_t)src | (uintptr_t)dst) & 15u) == 0) ? 1u : 0u;
-  uint64_t blocks = ((n + kPerLane - 1) / kPerLane + kThreads - 1) / kThreads;
+  uint64_t blocks = (n + Shape<DIR>::kSpan - 1) / Shape<DIR>::kSpan;
   if (blocks > kMaxFlatBlocks) blocks = kMaxFlatBlocks;
-  hipLaunchKernelGGL(codec_flat<DIR>, dim3((uint32_t)blocks), dim3(kThreads), 0,
+  hipLaunchKernelGGL(codec_flat<DIR>, dim3((uint32_t)blocks), dim3(Shape<DIR>::kLanes), 0,
                      (hipStream_t)stream, src, dst, n, vec);
   ARK_HIP(hipGetLastError());
   return ARK_OPT_OK;
@@ -187,7 +204,7 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      if (segs.size() > 0x7FFFFFFFu / kBlocksPerSeg)
+      if (segs.size() > 0x7FFFFFFFu / kMaxBlocksPerSeg)
         return ark::fail(ARK_OPT_EINVAL, "too many elements");
     }
   }
@@ -215,12 +232,15 @@ int ark_codec_plan_run(ark_codec_plan* p) {
   if (p->nseg == 0) return ARK_OPT_OK;
   ark::DeviceGuard g(p->device);
   if (!g.ok) return ark::fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
-  if (p->direction == ARK_CODEC_F16_TO_F32)
-    hipLaunchKernelGGL(codec_batch<ARK_CODEC_F16_TO_F32>, dim3(p->nseg * kBlocksPerSeg),
-                       dim3(kThreads), 0, p->stream, p->d_segs);
-  else
-    hipLaunchKernelGGL(codec_batch<ARK_CODEC_F32_TO_F16>, dim3(p->nseg * kBlocksPerSeg),
-                       dim3(kThreads), 0, p->stream, p->d_segs);
+  if (p->direction == ARK_CODEC_F16_TO_F32) {
+    typedef Shape<ARK_CODEC_F16_TO_F32> S;
+    hipLaunchKernelGGL(codec_batch<ARK_CODEC_F16_TO_F32>, dim3(p->nseg * S::kBlocksPerSeg),
+                       dim3(S::kLanes), 0, p->stream, p->d_segs);
+  } else {
+    typedef Shape<ARK_CODEC_F32_TO_F16> S;
+    hipLaunchKernelGGL(codec_batch<ARK_CODEC_F32_TO_F16>, dim3(p->nseg * S::kBlocksPerSeg),
+                       dim3(S::kLanes), 0, p->stream, p->d_segs);
+  }
   ARK_HIP(hipGetLastError());
   return ARK_OPT_OK;
 }
