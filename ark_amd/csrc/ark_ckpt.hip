@@ -49,13 +49,21 @@ constexpr uint64_t kFileHeaderV4 = 28;  // u32 magic + 3 x u64 (io.rs:453-456)
 constexpr uint64_t kRecHeaderV4 = 16;   // u64 n + u64 type (io.rs:460-461, :467-468)
 constexpr uint64_t kTrailerBytes = 40;  // u32 magic + u32 version + ark_opt_state
 constexpr uint32_t kTrailerVersion = 1;
-constexpr int kThreads = 256;
-// One 16-byte chunk or unit per lane per block (many small blocks stream
-// faster on MI355X than a few with several accesses per lane).
-constexpr uint32_t kPackSegBytes = 16 * kThreads;     // image bytes per pack block
-constexpr int kPackChunks = kPackSegBytes / (16 * kThreads);  // 1 per lane
-// elements per unpack block: one 16-byte unit of the file type per lane
-constexpr uint32_t unpack_seg(uint32_t ftype) { return (ftype == ARK_CKPT_F16 ? 8u : 4u) * kThreads; }
+constexpr int kThreads = 256;  // header and check kernels
+// Pack and unpack launch shapes: lanes per block, and 16-byte image chunks
+// (pack) or units (unpack) per lane, kLanes * 16 bytes apart.  Measured on
+// MI355X over the EKO-237M image: 256 lanes with one chunk per lane beat 64,
+// 128 and 512 lanes with one, two or four per lane (pack 0.91 ms against
+// 0.96-1.09 ms per call, unpack 0.94 against 0.95-0.99 ms).
+constexpr int kPackLanes = 256;
+constexpr int kPackChunks = 1;
+constexpr uint32_t kPackSegBytes = 16u * kPackLanes * kPackChunks;  // image bytes per block
+constexpr int kUnpackLanes = 256;
+constexpr int kUnpackUnits = 1;
+// elements per unpack block: kUnpackUnits 16-byte units of the file type per lane
+constexpr uint32_t unpack_seg(uint32_t ftype) {
+  return (ftype == ARK_CKPT_F16 ? 8u : 4u) * kUnpackLanes * kUnpackUnits;
+}
 constexpr size_t kStageBytes = (size_t)64 << 20;      // per pinned staging buffer
 static_assert(sizeof(ark_opt_state) == 32, "trailer holds a 32-byte state");
 
@@ -148,7 +156,7 @@ __device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start,
 
 // Block j of a tensor covers image bytes [base + j*S, base + (j+1)*S) of its
 // data, base = data_off rounded down to 16, clipped to the data.
-__global__ __launch_bounds__(kThreads) void pack_kernel(const PackRec* __restrict__ recs,
+__global__ __launch_bounds__(kPackLanes) void pack_kernel(const PackRec* __restrict__ recs,
                                                         const uint32_t* __restrict__ start,
                                                         uint32_t nrec, uint8_t* __restrict__ img) {
   const uint32_t r = find_rec(start, nrec, blockIdx.x);
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const PackRec* __restric
   const uint64_t seg_hi = c0 + kPackSegBytes < end ? c0 + kPackSegBytes : end;
 #pragma unroll
   for (int k = 0; k < kPackChunks; ++k) {
-    const uint64_t c = c0 + 16ull * (uint64_t)(k * kThreads + threadIdx.x);
+    const uint64_t c = c0 + 16ull * (uint64_t)(k * kPackLanes + threadIdx.x);
     if (c >= seg_hi) break;
     const uint64_t lo = c > seg_lo ? c : seg_lo;
     const uint64_t hi = c + 16 < seg_hi ? c + 16 : seg_hi;
@@ -246,7 +254,7 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
   constexpr uint32_t kFs = FT == ARK_CKPT_F16 ? 2u : 4u;  // file element bytes
   constexpr uint32_t kU = 16u / kFs;                       // elements per unit
   constexpr uint32_t kSegN = unpack_seg(FT);
-  constexpr int kUnits = (int)(kSegN / kU / kThreads);     // 1 per lane
+  constexpr int kUnits = (int)(kSegN / kU / kUnpackLanes);  // units per lane
   const uint32_t ds = s.dtype == ARK_CKPT_F16 ? 2u : 4u;
   const uint64_t src_off = s.src_off + e_begin * kFs;
   const uint32_t sh = (uint32_t)(src_off & 15u);
@@ -254,7 +262,7 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
   uint8_t* dst0 = (uint8_t*)s.dst + e_begin * ds;
 #pragma unroll
   for (int k = 0; k < kUnits; ++k) {
-    const uint32_t e0 = ((uint32_t)k * kThreads + threadIdx.x) * kU;
+    const uint32_t e0 = ((uint32_t)k * kUnpackLanes + threadIdx.x) * kU;
     if (e0 >= n) break;
     const uint64_t sb = src_off + (uint64_t)e0 * kFs;
     const uint64_t a0 = sb & ~15ull;
@@ -276,9 +284,9 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
   }
 }
 
-// Block j of a tensor converts its elements [j*S, (j+1)*S), S = 2048 for an
-// F16 file tensor and 1024 for F32 (one 16-byte unit per lane).
-__global__ __launch_bounds__(kThreads) void unpack_kernel(const UnpackRec* __restrict__ recs,
+// Block j of a tensor converts its elements [j*S, (j+1)*S), S = unpack_seg of
+// the tensor's file type.
+__global__ __launch_bounds__(kUnpackLanes) void unpack_kernel(const UnpackRec* __restrict__ recs,
                                                           const uint32_t* __restrict__ start,
                                                           uint32_t nrec,
                                                           const uint8_t* __restrict__ img,
@@ -487,7 +495,7 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
                      stream, dp, np, img);
   ARK_HIP(hipGetLastError());
   if (blocks) {
-    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, dr, dst,
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kPackLanes), 0, stream, dr, dst,
                        (uint32_t)n, img);
     ARK_HIP(hipGetLastError());
   }
@@ -531,7 +539,7 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
   }
   StreamSync sync{stream};
   ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
-  hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kUnpackLanes), 0, stream,
                      (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb), (uint32_t)n, img,
                      img_bytes);
   ARK_HIP(hipGetLastError());
