@@ -13,10 +13,16 @@
 //         1. keys_kernel: key = clamped token, value = position i;
 //         2. a stable LSD radix sort of (key, i) over the key's bits
 //            (hipCUB), which keeps equal keys in increasing i;
-//         3. run_kernel: one wave per (run of equal keys, 256-column tile)
-//            finds the run's end by binary search, loads the embedding row
-//            once, adds the run's dx0 rows in sorted (= original) order with
-//            32 rows' loads in flight at a time, and stores it once.
+//         3. gather_kernel: the dx0 rows copied in sorted order into a
+//            workspace, so every run of equal keys is contiguous;
+//         4. run_kernel: one 256-lane block per (run of equal keys,
+//            256-column tile) finds the run's end by binary search, loads the
+//            embedding row once, adds the run's rows in sorted (= original)
+//            order and stores it once.  A run of kLongRun rows or more gives
+//            each lane one column and keeps kColRows rows' loads in flight
+//            (the run is a sequential fp32 chain per column, so its time is
+//            load round trips); a shorter run is done by the first wave alone
+//            with 16-byte accesses.
 //       Every element therefore sees the same additions in the same order as
 //       the CPU loop, and the result is bit-identical.
 #include <string.h>
@@ -38,8 +44,13 @@ constexpr int kPerLane = 4;
 constexpr uint32_t kSeg = 4096;
 constexpr int kWave = 64;
 constexpr uint32_t kBlocksPerSeg = kSeg / (kWave * kPerLane);  // 16
-constexpr int kTileCols = kWave * kPerLane;                   // run_kernel: 256 columns per wave
-constexpr int kRowBatch = 32;                                 // dx0 rows in flight per wave
+constexpr int kTileCols = 256;  // run_kernel: columns per block
+constexpr int kLongRun = 8;     // runs of at least this many rows: one column per lane
+// Rows in flight per lane on a long run.  Measured on MI355X (4096 tokens,
+// d 768): 60 rows with one column per lane run a single 4096-row run in 73 us
+// against 400 us for 32 rows of four columns; more than 60 gain nothing, a
+// wave keeping at most 63 vector loads outstanding.
+constexpr int kColRows = 60;
 
 struct GradSeg {
   float* dst;
@@ -106,15 +117,30 @@ __global__ __launch_bounds__(kThreads) void keys_kernel(const uint32_t* __restri
   vals[i] = i;
 }
 
+// Row q of xs = row svals[q] of dx0 (d floats each); one block per row.
+// vec: d % 4 == 0 and dx0 16-byte aligned (xs is 256-byte aligned).
+__global__ __launch_bounds__(kThreads) void gather_kernel(const float* __restrict__ dx0,
+                                                          const uint32_t* __restrict__ svals,
+                                                          uint32_t d, uint32_t vec,
+                                                          float* __restrict__ xs) {
+  const float* src = dx0 + (uint64_t)svals[blockIdx.x] * d;
+  float* dst = xs + (uint64_t)blockIdx.x * d;
+  if (vec) {
+    for (uint32_t c = threadIdx.x * kPerLane; c < d; c += kThreads * kPerLane)
+      st_g<f32x4>(dst + c, ld_nt<f32x4>(src + c));
+  } else {
+    for (uint32_t c = threadIdx.x; c < d; c += kThreads) st_g<float>(dst + c, ld_g<float>(src + c));
+  }
+}
+
 // Block (p, tile): if sorted position p starts a run of equal keys, add the
-// run's dx0 rows (in sorted order, which is increasing i) into columns
-// [tile*256, tile*256 + 256) of the key's embedding row.  vec: d % 4 == 0
-// and both matrices 16-byte aligned.
-__global__ __launch_bounds__(64) void run_kernel(float* __restrict__ g, uint32_t d,
-                                                 const float* __restrict__ dx0,
-                                                 const uint32_t* __restrict__ skeys,
-                                                 const uint32_t* __restrict__ svals, uint32_t n,
-                                                 uint32_t vec) {
+// run's rows (xs rows p.., in sorted order, which is increasing i) into
+// columns [tile*256, tile*256 + 256) of the key's embedding row.  vec:
+// d % 4 == 0 and g 16-byte aligned.
+__global__ __launch_bounds__(kTileCols) void run_kernel(float* __restrict__ g, uint32_t d,
+                                                        const float* __restrict__ xs,
+                                                        const uint32_t* __restrict__ skeys,
+                                                        uint32_t n, uint32_t vec) {
   const uint32_t p = blockIdx.x;
   const uint32_t t = skeys[p];
   if (p > 0 && skeys[p - 1] == t) return;
@@ -127,34 +153,51 @@ __global__ __launch_bounds__(64) void run_kernel(float* __restrict__ g, uint32_t
     else
       hi = mid;
   }
-  const uint32_t e = hi;
+  const uint32_t len = hi - p;
+  const float* x = xs + (uint64_t)p * d;  // the run's rows, contiguous
+  if (len >= (uint32_t)kLongRun) {
+    const uint32_t c = blockIdx.y * kTileCols + threadIdx.x;
+    if (c >= d) return;
+    float* gp = g + (uint64_t)t * d + c;
+    float acc = ld_g<float>(gp);
+    uint32_t k = 0;
+    for (; k + kColRows <= len; k += kColRows) {
+      float v[kColRows];
+#pragma unroll
+      for (int j = 0; j < kColRows; ++j) v[j] = ld_g<float>(x + (uint64_t)(k + j) * d + c);
+#pragma unroll
+      for (int j = 0; j < kColRows; ++j) acc = acc + v[j];
+    }
+    for (; k < len; ++k) acc = acc + ld_g<float>(x + (uint64_t)k * d + c);
+    st_g<float>(gp, acc);
+    return;
+  }
+  if (threadIdx.x >= kWave) return;  // a short run: the first wave, four columns per lane
   const uint32_t c0 = blockIdx.y * kTileCols + threadIdx.x * kPerLane;
   if (c0 >= d) return;
-  float* grow = g + (uint64_t)t * d + c0;
+  float* gp = g + (uint64_t)t * d + c0;
   if (vec) {  // c0 + 4 <= d since d % 4 == 0
-    f32x4 acc = ld_g<f32x4>(grow);
-    for (uint32_t q = p; q < e; q += kRowBatch) {
-      f32x4 v[kRowBatch];
+    f32x4 acc = ld_g<f32x4>(gp);
+    f32x4 v[kLongRun - 1];
 #pragma unroll
-      for (int k = 0; k < kRowBatch; ++k)
-        if (q + k < e) v[k] = ld_nt<f32x4>(dx0 + (uint64_t)svals[q + k] * d + c0);
+    for (int j = 0; j < kLongRun - 1; ++j)
+      if ((uint32_t)j < len) v[j] = ld_g<f32x4>(x + (uint64_t)j * d + c0);
 #pragma unroll
-      for (int k = 0; k < kRowBatch; ++k) {
-        if (q + k < e) {
-          acc.x = acc.x + v[k].x;
-          acc.y = acc.y + v[k].y;
-          acc.z = acc.z + v[k].z;
-          acc.w = acc.w + v[k].w;
-        }
+    for (int j = 0; j < kLongRun - 1; ++j) {
+      if ((uint32_t)j < len) {
+        acc.x = acc.x + v[j].x;
+        acc.y = acc.y + v[j].y;
+        acc.z = acc.z + v[j].z;
+        acc.w = acc.w + v[j].w;
       }
     }
-    st_g<f32x4>(grow, acc);
+    st_g<f32x4>(gp, acc);
   } else {
     const int nc = d - c0 < (uint32_t)kPerLane ? (int)(d - c0) : kPerLane;
     for (int c = 0; c < nc; ++c) {
-      float acc = ld_g<float>(grow + c);
-      for (uint32_t q = p; q < e; ++q) acc = acc + ld_g<float>(dx0 + (uint64_t)svals[q] * d + c0 + c);
-      st_g<float>(grow + c, acc);
+      float acc = ld_g<float>(gp + c);
+      for (uint32_t j = 0; j < len; ++j) acc = acc + ld_g<float>(x + (uint64_t)j * d + c0 + c);
+      st_g<float>(gp + c, acc);
     }
   }
 }
@@ -303,26 +346,32 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
                                              (uint32_t*)nullptr, (const uint32_t*)nullptr,
                                              (uint32_t*)nullptr, n, 0, end_bit, s));
   const size_t arr = ark::align_up((size_t)batch_seq * 4, 256);
+  const size_t rows = ark::align_up((size_t)xbytes, 256);
+  const size_t ws_bytes = 4 * arr + rows + temp;
   StreamBuf ws;
-  hipError_t e = ws.alloc(4 * arr + temp + 256, s);
+  hipError_t e = ws.alloc(ws_bytes, s);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", 4 * arr + temp);
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", ws_bytes);
   }
   uint32_t* keys = (uint32_t*)ws.p;
   uint32_t* vals = (uint32_t*)((char*)ws.p + arr);
   uint32_t* skeys = (uint32_t*)((char*)ws.p + 2 * arr);
   uint32_t* svals = (uint32_t*)((char*)ws.p + 3 * arr);
-  void* tmp = (char*)ws.p + 4 * arr;
+  float* xs = (float*)((char*)ws.p + 4 * arr);
+  void* tmp = (char*)ws.p + 4 * arr + rows;
   hipLaunchKernelGGL(keys_kernel, dim3((batch_seq + kThreads - 1) / kThreads), dim3(kThreads), 0,
                      s, tokens, batch_seq, vocab, keys, vals);
   ARK_HIP(hipGetLastError());
   ARK_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, temp, keys, skeys, vals, svals, n, 0, end_bit,
                                              s));
-  const uint32_t vec =
-      ((d % 4u) == 0 && ((((uintptr_t)embed_grad | (uintptr_t)dx0) & 15u) == 0)) ? 1u : 0u;
+  const uint32_t gvec = ((d % 4u) == 0 && (((uintptr_t)dx0 & 15u) == 0)) ? 1u : 0u;
+  hipLaunchKernelGGL(gather_kernel, dim3(batch_seq), dim3(kThreads), 0, s, dx0, svals, d, gvec,
+                     xs);
+  ARK_HIP(hipGetLastError());
+  const uint32_t vec = ((d % 4u) == 0 && (((uintptr_t)embed_grad & 15u) == 0)) ? 1u : 0u;
   const dim3 grid(batch_seq, (d + kTileCols - 1) / kTileCols);
-  hipLaunchKernelGGL(run_kernel, grid, dim3(64), 0, s, embed_grad, d, dx0, skeys, svals,
+  hipLaunchKernelGGL(run_kernel, grid, dim3(kTileCols), 0, s, embed_grad, d, xs, skeys,
                      batch_seq, vec);
   ARK_HIP(hipGetLastError());
   return ARK_OPT_OK;

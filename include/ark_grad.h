@@ -47,10 +47,11 @@ int ark_grad_plan_destroy(ark_grad_plan *plan);
  * t = tokens[i] < vocab ? tokens[i] : 0,
  *     embed_grad[t*d + j] += dx0[i*d + j]   for j < d.
  * Every element receives its additions in increasing i, as in the loop: the
- * positions are stably sorted by token on the device and one wave adds each
- * token's rows in order.  embed_grad holds vocab*d floats, dx0 batch_seq*d,
- * tokens batch_seq.  Stream ordered; the scratch it needs (16 B per token
- * plus the sort's) comes from the stream-ordered pool. */
+ * positions are stably sorted by token on the device, the dx0 rows copied in
+ * that order, and each token's rows added in order, column by column.
+ * embed_grad holds vocab*d floats, dx0 batch_seq*d, tokens batch_seq.
+ * Stream ordered; the scratch it needs (a copy of dx0, 16 B per token and
+ * the sort's) comes from the stream-ordered pool. */
 int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
                            const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                            void *stream);

@@ -66,6 +66,29 @@ def test_scatter_one_long_run_and_order():
     np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("d", [768, 770, 5])
+def test_scatter_run_lengths_at_the_path_boundaries(d):
+    """Runs of 1, 7 and 8 rows (the short and long paths meet at 8) and of
+    59, 60, 61, 120, 121 and 500 rows (the long path adds 60 rows per round,
+    then a tail), positions shuffled, against the oracle."""
+    torch = _torch()
+    rng = np.random.default_rng(d)
+    lengths = [1, 7, 8, 59, 60, 61, 120, 121, 500]
+    vocab = 1000
+    ids = rng.choice(vocab, len(lengths), replace=False)
+    tokens = np.concatenate([np.full(k, t, np.uint32) for k, t in zip(lengths, ids)])
+    tokens = tokens[rng.permutation(len(tokens))]
+    n = len(tokens)
+    dx0 = (rng.standard_normal((n, d)) * 10.0 ** rng.integers(-4, 4, (n, 1))).astype(np.float32)
+    g = rng.standard_normal((vocab, d)).astype(np.float32)
+    want = g.copy()
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.from_numpy(g).cuda()
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
 def test_scatter_unaligned_rows_take_the_scalar_path():
     torch = _torch()
     vocab, d, n = 300, 64, 500
