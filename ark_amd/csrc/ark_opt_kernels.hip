@@ -468,9 +468,16 @@ template <typename GT>
 __global__ __launch_bounds__(64) void adamw_kernel(
     const SegDesc* __restrict__ segs, const StepScalars* __restrict__ scal,
     float beta1, float beta2, float eps) {
-  const StepScalars sc = *scal;
+  SegDesc d = segs[blockIdx.x / kRowsPerSeg];
+  StepScalars sc = *scal;
+  // Every field used below is in registers before the first branch, so the
+  // wave waits for one round trip of scalar loads rather than a chain of
+  // them (left alone, the compiler loads the step scalars, branches, then
+  // loads the descriptor).
+  asm volatile("" : "+s"(d.w), "+s"(d.g), "+s"(d.m), "+s"(d.v), "+s"(d.n), "+s"(d.wd),
+               "+s"(d.flags), "+s"(sc.applied), "+s"(sc.inv), "+s"(sc.coef), "+s"(sc.lr),
+               "+s"(sc.lr_eff), "+s"(sc.c1), "+s"(sc.c2));
   if (!sc.applied) return;  // skipped step: training.rs:293-305
-  const SegDesc d = segs[blockIdx.x / kRowsPerSeg];
   const uint32_t r0 = (blockIdx.x % kRowsPerSeg) * kRow;
   if (r0 >= d.n) return;  // row past the end of a short segment
   const uint32_t valid = d.n - r0 < (uint32_t)kRow ? d.n - r0 : (uint32_t)kRow;
