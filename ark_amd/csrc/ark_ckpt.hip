@@ -50,6 +50,7 @@ constexpr uint64_t kRecHeaderV4 = 16;   // u64 n + u64 type (io.rs:460-461, :467
 constexpr uint64_t kTrailerBytes = 40;  // u32 magic + u32 version + ark_opt_state
 constexpr uint32_t kTrailerVersion = 1;
 constexpr int kThreads = 256;  // header and check kernels
+constexpr uint32_t kHintShift = 8;  // pack/unpack blocks per find_rec hint: 256
 // Pack and unpack launch shapes: lanes per block, and 16-byte image chunks
 // (pack) or units (unpack) per lane, kLanes * 16 bytes apart.  Measured on
 // MI355X over the EKO-237M image: 256 lanes with one chunk per lane beat 64,
@@ -140,10 +141,14 @@ __global__ __launch_bounds__(kThreads) void header_kernel(const HdrPiece* __rest
   for (uint32_t b = 0; b < p.len; ++b) st_u8(img + p.off + b, p.bytes[b]);
 }
 
-// The tensor that block b belongs to (see PackRec).
-__device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start, uint32_t nrec,
-                                             uint32_t b) {
-  uint32_t lo = 0, hi = nrec;  // start[lo] <= b < start[hi]
+// The tensor that block b belongs to (see PackRec).  hint[i] is the tensor
+// holding block min(i << kHintShift, blocks - 1) (make_hints), so the search
+// runs between two neighbouring hints: mostly zero to two steps, where a
+// search over the whole table would chain ten dependent loads per block.
+__device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start,
+                                             const uint32_t* __restrict__ hint, uint32_t b) {
+  const uint32_t i = b >> kHintShift;
+  uint32_t lo = hint[i], hi = hint[i + 1] + 1;  // start[lo] <= b < start[hi]
   while (hi - lo > 1) {
     const uint32_t mid = (lo + hi) >> 1;
     if (start[mid] <= b)
@@ -157,9 +162,10 @@ __device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start,
 // Block j of a tensor covers image bytes [base + j*S, base + (j+1)*S) of its
 // data, base = data_off rounded down to 16, clipped to the data.
 __global__ __launch_bounds__(kPackLanes) void pack_kernel(const PackRec* __restrict__ recs,
-                                                        const uint32_t* __restrict__ start,
-                                                        uint32_t nrec, uint8_t* __restrict__ img) {
-  const uint32_t r = find_rec(start, nrec, blockIdx.x);
+                                                          const uint32_t* __restrict__ start,
+                                                          const uint32_t* __restrict__ hint,
+                                                          uint8_t* __restrict__ img) {
+  const uint32_t r = find_rec(start, hint, blockIdx.x);
   const PackRec s = recs[r];
   const uint64_t base = s.data_off & ~15ull;
   const uint64_t end = s.data_off + s.src_bytes;
@@ -287,11 +293,11 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
 // Block j of a tensor converts its elements [j*S, (j+1)*S), S = unpack_seg of
 // the tensor's file type.
 __global__ __launch_bounds__(kUnpackLanes) void unpack_kernel(const UnpackRec* __restrict__ recs,
-                                                          const uint32_t* __restrict__ start,
-                                                          uint32_t nrec,
-                                                          const uint8_t* __restrict__ img,
-                                                          uint64_t img_bytes) {
-  const uint32_t r = find_rec(start, nrec, blockIdx.x);
+                                                            const uint32_t* __restrict__ start,
+                                                            const uint32_t* __restrict__ hint,
+                                                            const uint8_t* __restrict__ img,
+                                                            uint64_t img_bytes) {
+  const uint32_t r = find_rec(start, hint, blockIdx.x);
   const UnpackRec s = recs[r];
   const uint64_t e_begin = (uint64_t)(blockIdx.x - start[r]) * unpack_seg(s.ftype);
   if (s.ftype == ARK_CKPT_F16)
@@ -338,6 +344,22 @@ struct DevBuf {
 };
 // Stream-ordered allocation from the device's default memory pool (no
 // device-wide synchronisation on free), for the small descriptor tables.
+// hint[i] = the tensor holding block min(i << kHintShift, blocks - 1), for
+// i = 0 .. ceil(blocks / 2^kHintShift): the last r with start[r] <= that
+// block, as find_rec defines it.  blocks >= 1.
+std::vector<uint32_t> make_hints(const std::vector<uint32_t>& start, uint32_t nrec,
+                                 uint64_t blocks) {
+  const uint64_t nh = (blocks + (1u << kHintShift) - 1) >> kHintShift;
+  std::vector<uint32_t> h((size_t)nh + 1);
+  uint32_t r = 0;
+  for (uint64_t i = 0; i <= nh; ++i) {
+    const uint64_t b = (i << kHintShift) < blocks ? (i << kHintShift) : blocks - 1;
+    while (r + 1 < nrec && start[r + 1] <= b) ++r;
+    h[(size_t)i] = r;
+  }
+  return h;
+}
+
 struct StreamBuf {
   void* p = nullptr;
   hipStream_t s = nullptr;
@@ -471,13 +493,16 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
     memcpy(tr + 8, amp, sizeof(ark_opt_state));
     put_bytes(pieces, L.end, tr, kTrailerBytes);
   }
-  // one upload: header pieces | tensor table | block starts
+  // one upload: header pieces | tensor table | block starts | hints
+  const std::vector<uint32_t> hint =
+      blocks ? make_hints(start, (uint32_t)n, blocks) : std::vector<uint32_t>();
   const size_t pb = pieces.size() * sizeof(HdrPiece), rb = recs.size() * sizeof(PackRec);
-  const size_t stb = start.size() * sizeof(uint32_t);
-  std::vector<uint8_t> host(pb + rb + stb);
+  const size_t stb = start.size() * sizeof(uint32_t), hb = hint.size() * sizeof(uint32_t);
+  std::vector<uint8_t> host(pb + rb + stb + hb);
   memcpy(host.data(), pieces.data(), pb);
   if (rb) memcpy(host.data() + pb, recs.data(), rb);
   memcpy(host.data() + pb + rb, start.data(), stb);
+  if (hb) memcpy(host.data() + pb + rb + stb, hint.data(), hb);
   StreamBuf d;
   hipError_t e = d.alloc(host.size(), stream);
   if (e != hipSuccess) {
@@ -489,6 +514,7 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
   HdrPiece* dp = (HdrPiece*)d.p;
   const PackRec* dr = (const PackRec*)((char*)d.p + pb);
   const uint32_t* dst = (const uint32_t*)((char*)d.p + pb + rb);
+  const uint32_t* dhint = (const uint32_t*)((char*)d.p + pb + rb + stb);
   ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
   const uint32_t np = (uint32_t)pieces.size();
   hipLaunchKernelGGL(header_kernel, dim3((np + kThreads - 1) / kThreads), dim3(kThreads), 0,
@@ -496,7 +522,7 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
   ARK_HIP(hipGetLastError());
   if (blocks) {
     hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kPackLanes), 0, stream, dr, dst,
-                       (uint32_t)n, img);
+                       dhint, img);
     ARK_HIP(hipGetLastError());
   }
   ARK_HIP(hipStreamSynchronize(stream));
@@ -526,10 +552,13 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
   }
   start[n] = (uint32_t)blocks;
   if (blocks == 0) return ARK_OPT_OK;
+  const std::vector<uint32_t> hint = make_hints(start, (uint32_t)n, blocks);
   const size_t rb = recs.size() * sizeof(UnpackRec), stb = start.size() * sizeof(uint32_t);
-  std::vector<uint8_t> host(rb + stb);
+  const size_t hb = hint.size() * sizeof(uint32_t);
+  std::vector<uint8_t> host(rb + stb + hb);
   memcpy(host.data(), recs.data(), rb);
   memcpy(host.data() + rb, start.data(), stb);
+  memcpy(host.data() + rb + stb, hint.data(), hb);
   StreamBuf d;
   hipError_t e = d.alloc(host.size(), stream);
   if (e != hipSuccess) {
@@ -540,8 +569,8 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
   StreamSync sync{stream};
   ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
   hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kUnpackLanes), 0, stream,
-                     (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb), (uint32_t)n, img,
-                     img_bytes);
+                     (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb),
+                     (const uint32_t*)((char*)d.p + rb + stb), img, img_bytes);
   ARK_HIP(hipGetLastError());
   ARK_HIP(hipStreamSynchronize(stream));
   return ARK_OPT_OK;
