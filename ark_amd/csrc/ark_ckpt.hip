@@ -186,6 +186,10 @@ __global__ __launch_bounds__(kPackLanes) void pack_kernel(const PackRec* __restr
         st_nt<u32x4>(img + c, ld_nt<u32x4>(s.src + a0));
         continue;
       }
+      if ((sh & 3u) == 0) {  // dword aligned: one 16-byte load
+        st_nt<u32x4>(img + c, (u32x4)ld_nt<u32x4_a4>(s.src + so));
+        continue;
+      }
       if (a0 + 32 <= s.src_bytes) {
         const u32x4 a = ld_nt<u32x4>(s.src + a0);
         const u32x4 b = ld_nt<u32x4>(s.src + a0 + 16);
@@ -276,6 +280,10 @@ __device__ __forceinline__ void unpack_block(const UnpackRec& s, uint64_t e_begi
     if (s.dst_vec && e0 + kU <= n) {
       if (sh == 0) {
         store_unit<FT>(ld_nt<u32x4>(img + a0), s.dtype, dst);
+        continue;
+      }
+      if ((sh & 3u) == 0) {  // dword aligned: one 16-byte load
+        store_unit<FT>((u32x4)ld_nt<u32x4_a4>(img + sb), s.dtype, dst);
         continue;
       }
       if (a0 + 32 <= img_bytes) {

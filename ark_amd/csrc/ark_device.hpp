@@ -14,6 +14,9 @@ namespace dev {
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16 bytes at a 4-byte-aligned address: the compiler emits one dwordx4
+// access where the target allows dword alignment, as gfx950 does.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 template <typename T>
 __device__ __forceinline__ T ld_nt(const void* p) {
