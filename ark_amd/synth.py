@@ -1,8 +1,33 @@
 """Seeded synthetic inputs on the device (include/ark_synth.h) for torch
-tensors: fp16 weights and loss-scaled fp16 gradients of the EKO shapes."""
+tensors: fp16 weights and loss-scaled fp16 gradients of the EKO shapes, and
+the parameter sets built from them (BASELINE's synthetic workloads).
+
+Streams of the generator: weights use (tensor_id = i, step = WEIGHT_STEP);
+gradients of step k use (tensor_id = i, step = k).  The CPU oracle builds the
+same inputs from the same counter-based generator, so both sides start from
+identical bits.
+"""
 import ctypes as C
 
+import numpy as np
+
+from . import _abi
 from ._lib import check, lib
+
+WEIGHT_STEP = 0xFFFFFFFF
+W_SIGMA = 0.02   # weights ~ N(0, 0.02)
+F16_ONE = 0x3C00  # RMSNorm gains start at 1.0
+
+
+def grad_sigma_scale(sigma, loss_scale):
+    """sigma * loss_scale rounded to fp32 (the generator's scale)."""
+    return float(np.float32(np.float32(sigma) * np.float32(loss_scale)))
+
+
+def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
+    """Per-tensor sigma = 10^U(lo, hi), drawn on the host (BASELINE c2)."""
+    rng = np.random.default_rng(seed)
+    return [float(np.float32(10.0 ** rng.uniform(lo, hi))) for _ in range(n)]
 
 
 def _stream(t):
@@ -33,3 +58,29 @@ def copy(dst, src):
 def fill_u16(t, bits):
     assert t.is_cuda and t.is_contiguous() and t.element_size() == 2
     check(lib().ark_synth_fill_u16(t.data_ptr(), t.numel(), bits, _stream(t)))
+
+
+def problem(specs, seed, weight_decay, sigmas, loss_scale, step=0, grad_dtype=_abi.GRAD_F16,
+            no_unscale=(), device="cuda"):
+    """A ParamSet of `specs` on the device: fp16 weights N(0, W_SIGMA) (gains
+    1.0), gradients N(0, sigma_i) * loss_scale of step `step`, m = v = 0."""
+    from .optimizer import ParamSet
+    ps = ParamSet(specs, weight_decay, device=device, grad_dtype=grad_dtype,
+                  no_unscale=no_unscale)
+    for i, s in enumerate(specs):
+        if s.gain:
+            fill_u16(ps.w(i), F16_ONE)
+        else:
+            normal_f16(ps.w(i), seed, i, WEIGHT_STEP, W_SIGMA)
+    regen_grads(ps, seed, sigmas, loss_scale, step)
+    return ps
+
+
+def regen_grads(ps, seed, sigmas, loss_scale, step):
+    """The gradients of step `step` into every tensor of the ParamSet."""
+    for i in range(len(ps)):
+        ss = grad_sigma_scale(sigmas[i], loss_scale)
+        if ps.grad_dtype == _abi.GRAD_F16:
+            normal_f16(ps.g(i), seed, i, step, ss)
+        else:
+            normal_f32(ps.g(i), seed, i, step, ss)

@@ -45,10 +45,10 @@ def log(msg):
 
 
 def sigmas_for(name, specs):
-    from oracle import harness as H  # only for the shared sigma draw (pure numpy)
+    from ark_amd import synth
     w = WORKLOADS[name]
     if w["sigma"] == "loguniform":
-        return H.log_uniform_sigmas(len(specs), SEED)
+        return synth.log_uniform_sigmas(len(specs), SEED)
     return [w["sigma"]] * len(specs)
 
 
@@ -64,9 +64,9 @@ def run_gpu(name, steps, warmup):
 
 def _run_gpu(name, steps, warmup, stream):
     import torch
+    from ark_amd import synth
     from ark_amd.eko import config_tensors
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
-    from oracle import harness as H
 
     specs = config_tensors(name)
     w = WORKLOADS[name]
@@ -74,7 +74,7 @@ def _run_gpu(name, steps, warmup, stream):
     cfg = AdamConfig(**HP)
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
-    ps = H.gpu_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
+    ps = synth.problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
     opt = Optimizer(cfg, ps, amp)
     torch.cuda.synchronize()
     _, info = opt.step_all(cfg.lr, info=True)

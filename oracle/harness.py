@@ -2,35 +2,22 @@
 tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
 
 A problem is a list of TensorSpec (ark_amd.eko) with seeded inputs built by
-the same counter-based generator on both sides (include/ark_synth.h on the
-GPU, oracle.synth_* on the CPU), so both start from identical bits.
-
-Streams of the generator: weights use (tensor_id = i, step = WEIGHT_STEP);
-gradients of step k use (tensor_id = i, step = k).
+the same counter-based generator on both sides (ark_amd.synth on the GPU,
+oracle.synth_* on the CPU), so both start from identical bits; the stream
+constants and the sigma draw are ark_amd.synth's.
 """
 import numpy as np
 
 import oracle
 from ark_amd import _abi
-
-WEIGHT_STEP = 0xFFFFFFFF
-W_SIGMA = 0.02
-F16_ONE = 0x3C00
+from ark_amd.synth import (F16_ONE, W_SIGMA, WEIGHT_STEP, grad_sigma_scale,  # noqa: F401
+                           log_uniform_sigmas)
+from ark_amd.synth import problem as gpu_problem  # noqa: F401
+from ark_amd.synth import regen_grads as gpu_regen_grads  # noqa: F401
 
 
 def f32(x):
     return float(np.float32(x))
-
-
-def grad_sigma_scale(sigma, loss_scale):
-    """sigma * loss_scale rounded to fp32 (both sides use this value)."""
-    return float(np.float32(np.float32(sigma) * np.float32(loss_scale)))
-
-
-def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
-    """Per-tensor sigma = 10^U(lo, hi), drawn on the host (BASELINE c2)."""
-    rng = np.random.default_rng(seed)
-    return [float(np.float32(10.0 ** rng.uniform(lo, hi))) for _ in range(n)]
 
 
 # ---- host side ----------------------------------------------------------------
@@ -75,32 +62,7 @@ def host_regen_grads(ts, seed, sigmas, loss_scale, step, grad_dtype=_abi.GRAD_F1
     _pmap(regen, range(len(ts)), nthreads)
 
 
-# ---- GPU side -----------------------------------------------------------------
-
-def gpu_problem(specs, seed, weight_decay, sigmas, loss_scale, step=0,
-                grad_dtype=_abi.GRAD_F16, no_unscale=(), device="cuda"):
-    from ark_amd import synth
-    from ark_amd.optimizer import ParamSet
-    ps = ParamSet(specs, weight_decay, device=device, grad_dtype=grad_dtype,
-                  no_unscale=no_unscale)
-    for i, s in enumerate(specs):
-        if s.gain:
-            synth.fill_u16(ps.w(i), F16_ONE)
-        else:
-            synth.normal_f16(ps.w(i), seed, i, WEIGHT_STEP, W_SIGMA)
-    gpu_regen_grads(ps, seed, sigmas, loss_scale, step)
-    return ps
-
-
-def gpu_regen_grads(ps, seed, sigmas, loss_scale, step):
-    from ark_amd import synth
-    for i in range(len(ps)):
-        ss = grad_sigma_scale(sigmas[i], loss_scale)
-        if ps.grad_dtype == _abi.GRAD_F16:
-            synth.normal_f16(ps.g(i), seed, i, step, ss)
-        else:
-            synth.normal_f32(ps.g(i), seed, i, step, ss)
-
+# ---- comparisons -------------------------------------------------------------
 
 def to_host(t):
     """torch tensor on the GPU -> numpy array with the same bits."""
