@@ -250,6 +250,44 @@ def test_single_tensor_dropin_matches_reference_kernel():
         assert not np.any(H.bits_differ32(dv.cpu().numpy()[off:], vv))
 
 
+@pytest.mark.parametrize("true_grads,clipped", [
+    ([0.5, -0.5, 0.5, 0.5], 0),          # norm exactly 1.0 = grad_clip: `>` is strict
+    ([1.0 + 2.0 ** -10], 1),             # just above: coef = 1 / norm
+    ([1.0 - 2.0 ** -11], 0),             # just below
+    ([0.0] * 9, 0),                      # norm 0
+])
+def test_clip_boundary_matches_oracle(true_grads, clipped):
+    """optimizer.rs:148-149 at the threshold (grad_clip 1.0, loss scale 1024),
+    one tensor of these gradients among 4096 zeros; every scalar and every
+    w/m/v bit against the oracle."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    scale = 1024.0
+    g = np.zeros(4096 + len(true_grads))
+    g[-len(true_grads):] = np.asarray(true_grads) * scale
+    g16 = g.astype(np.float16)
+    assert np.array_equal(g16.astype(np.float64), g)
+    n = g.size
+    rng = np.random.default_rng(n)
+    w = (rng.standard_normal(n) * 0.02).astype(np.float16).view(np.uint16)
+    specs = [TensorSpec("a", (n,), True, False)]
+    cfg = AdamConfig(**HP)
+    ps = ParamSet(specs, cfg.weight_decay)
+    ps.w(0).copy_(torch.from_numpy(w.view(np.int16)).view(torch.float16))
+    ps.g(0).copy_(torch.from_numpy(g16))
+    ts = [oracle.HostTensor(w.copy(), g16.view(np.uint16).copy(), np.zeros(n, np.float32),
+                            np.zeros(n, np.float32), cfg.weight_decay)]
+    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=scale))
+    ref = oracle.Optimizer(ts, opt.hp)
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert not H.info_matches(gi, ri)
+    assert gi.clipped == clipped and (clipped or gi.clip_coef == 1.0)
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0, c
+    opt.close()
+
+
 def test_edge_values_weights_near_overflow_and_subnormal_grads():
     """Weights near 65504 (overflow to inf on requantisation), fp16
     subnormal weights and gradients, zero gradients."""
