@@ -211,6 +211,57 @@ def test_growth_cap_and_early_stop():
     opt.close()
 
 
+def test_finite_flag_every_fp16_pattern():
+    """training.rs:291 on the device, exhaustively: each of the 2048 inf/NaN
+    fp16 patterns, alone among zeros, makes the step skip -- placed in a
+    tensor of eight full segments (one norm block of vector loads) or in a
+    ragged one (mixed block, element-wise tail) at varying positions; and a
+    tensor holding all 63,488 finite patterns applies, with every scalar and
+    every w/m/v bit equal to the oracle's."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    allp = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    nonfin = allp[(allp & 0x7C00) == 0x7C00]
+    finite = allp[(allp & 0x7C00) != 0x7C00]
+    assert nonfin.size == 2048 and finite.size == 63488
+    cfg = AdamConfig(**HP)
+    amp = AmpConfig(loss_scale_init=1.0, max_consecutive_nonfinite=1 << 30)
+    specs = [TensorSpec("full", (8 * 4096,), True, False), TensorSpec("ragged", (4133,), True, False)]
+    ps = ParamSet(specs, cfg.weight_decay)
+    opt = Optimizer(cfg, ps, amp)
+    gi = None
+    for i, p in enumerate(nonfin):
+        t = i & 1
+        pos = (i * 131) % specs[t].n if t == 0 else (i * 97) % specs[t].n
+        g = ps.g(t).view(torch.int16)
+        g[pos] = int(np.array(p, np.uint16).view(np.int16))
+        _, gi = opt.step_all(cfg.lr, info=True)
+        assert gi.applied == 0 and gi.nonfinite == 1, (hex(int(p)), t, pos)
+        g[pos] = 0
+    assert gi.state.skipped_steps == 2048 and gi.state.t == 0
+    opt.close()
+
+    n = finite.size
+    specs = [TensorSpec("finite", (n,), True, False)]
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal(n) * 0.02).astype(np.float16).view(np.uint16)
+    g = rng.permutation(finite)
+    ps = ParamSet(specs, cfg.weight_decay)
+    ps.w(0).copy_(torch.from_numpy(w.view(np.int16)).view(torch.float16))
+    ps.g(0).copy_(torch.from_numpy(g.view(np.int16)).view(torch.float16))
+    ts = [oracle.HostTensor(w.copy(), g.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32),
+                            cfg.weight_decay)]
+    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=1.0))
+    ref = oracle.Optimizer(ts, opt.hp)
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert gi.applied == 1 and gi.nonfinite == 0
+    assert not H.info_matches(gi, ri)
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0, c
+    opt.close()
+
+
 def test_record_overflow_matches_oracle():
     specs = [TensorSpec("a", (512,), True, False)]
     sig = [1e-3]
