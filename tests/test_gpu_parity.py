@@ -262,6 +262,30 @@ def test_finite_flag_every_fp16_pattern():
     opt.close()
 
 
+@pytest.mark.parametrize("bits,skips", [(0x7F800000, 1), (0xFF800000, 1), (0x7FC00000, 1),
+                                        (0x7F800001, 1), (0xFFFFFFFF, 1), (0x7F7FFFFF, 0),
+                                        (0x00000001, 0)])
+def test_fp32_gradient_special_values(bits, skips):
+    """ARK_OPT_GRAD_F32 (the reference's own fp32 gradients): infinities
+    and quiet, signalling and negative NaNs skip the step; the largest finite
+    value (its square overflows fp32, not the f64 norm) and the smallest
+    subnormal apply; placed in the vector rows and in the ragged tail; every
+    scalar and w/m/v bit against the oracle."""
+    torch = _torch()
+    specs = [TensorSpec("a", (4096 * 3,), True, False), TensorSpec("b", (777,), True, False)]
+    cfg, ps, ts, opt, ref = _make(specs, 4, [1e-3, 1e-3], 1.0, grad_dtype=_abi.GRAD_F32)
+    for ti, pos in [(0, 5000), (1, 770)]:
+        ps.g(ti).view(torch.int32)[pos] = int(np.array(bits, np.uint32).view(np.int32))
+        ts[ti].g.view(np.uint32)[pos] = bits
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert gi.applied == 1 - skips and gi.nonfinite == skips
+    assert not H.info_matches(gi, ri)
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0, c
+    opt.close()
+
+
 def test_record_overflow_matches_oracle():
     specs = [TensorSpec("a", (512,), True, False)]
     sig = [1e-3]
