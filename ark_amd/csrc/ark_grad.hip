@@ -10,9 +10,11 @@
 //   embed scatter  the loop of bridge.m:922-928 adds row i of dx0 into the
 //       embedding row of token i, in increasing i.  Atomics would add in an
 //       arbitrary order and change the fp32 sums, so instead:
-//         1. keys_kernel: key = clamped token, value = position i;
-//         2. a stable LSD radix sort of (key, i) over the key's bits
-//            (hipCUB), which keeps equal keys in increasing i;
+//         1. key = clamped token, value = position i, and a stable LSD radix
+//            sort of (key, i) over the key's bits, which keeps equal keys in
+//            increasing i: for up to kBlockSortMax tokens (the reference's
+//            2 x 2048 batch) one block sorts them in LDS (block_sort_kernel),
+//            beyond that keys_kernel and hipCUB's device radix sort;
 //         3. gather_kernel: the dx0 rows copied in sorted order into a
 //            workspace, so every run of equal keys is contiguous;
 //         4. run_kernel: one 256-lane block per (run of equal keys,
@@ -102,6 +104,45 @@ __global__ __launch_bounds__(kWave) void grad_batch(const GradSeg* __restrict__ 
   } else {
     for (int j = 0; j < kPerLane; ++j)
       if (e0 + j < d.n) add1(d.dst + e0 + j, d.src + e0 + j);
+  }
+}
+
+// Up to kBlockSortMax tokens: one block loads them (key = clamped token,
+// value = position, bridge.m:923), sorts the pairs over bits [0, end_bit)
+// with the stable block radix sort, and writes them out.  Input and output
+// are in blocked order (thread t holds positions t*kSortItems..), so the
+// stable sort keeps equal keys in increasing position.  Padding past n takes
+// the all-ones key: it ties with the largest real key at most and, coming
+// later in the input, sorts after it.
+constexpr int kSortThreads = 1024;
+constexpr int kSortItems = 4;
+constexpr uint32_t kBlockSortMax = kSortThreads * kSortItems;  // 4096
+
+__global__ __launch_bounds__(kSortThreads) void block_sort_kernel(
+    const uint32_t* __restrict__ tokens, uint32_t n, uint32_t vocab, int end_bit,
+    uint32_t* __restrict__ skeys, uint32_t* __restrict__ svals) {
+  typedef hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortItems, uint32_t> Sort;
+  __shared__ typename Sort::TempStorage tmp;
+  uint32_t k[kSortItems], v[kSortItems];
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t i = threadIdx.x * kSortItems + j;
+    uint32_t t = 0xFFFFFFFFu;
+    if (i < n) {
+      t = ld_g<uint32_t>(tokens + i);
+      t = t < vocab ? t : 0u;
+    }
+    k[j] = t;
+    v[j] = i;
+  }
+  Sort(tmp).Sort(k, v, 0, end_bit);
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t i = threadIdx.x * kSortItems + j;
+    if (i < n) {
+      skeys[i] = k[j];
+      svals[i] = v[j];
+    }
   }
 }
 
@@ -341,10 +382,12 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
   int end_bit = 1;
   while (end_bit < 32 && ((vocab - 1u) >> end_bit) != 0u) ++end_bit;
   const int n = (int)batch_seq;
+  const bool block_sort = batch_seq <= kBlockSortMax;
   size_t temp = 0;
-  ARK_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (const uint32_t*)nullptr,
-                                             (uint32_t*)nullptr, (const uint32_t*)nullptr,
-                                             (uint32_t*)nullptr, n, 0, end_bit, s));
+  if (!block_sort)
+    ARK_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (const uint32_t*)nullptr,
+                                               (uint32_t*)nullptr, (const uint32_t*)nullptr,
+                                               (uint32_t*)nullptr, n, 0, end_bit, s));
   const size_t arr = ark::align_up((size_t)batch_seq * 4, 256);
   const size_t rows = ark::align_up((size_t)xbytes, 256);
   const size_t ws_bytes = 4 * arr + rows + temp;
@@ -360,11 +403,17 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
   uint32_t* svals = (uint32_t*)((char*)ws.p + 3 * arr);
   float* xs = (float*)((char*)ws.p + 4 * arr);
   void* tmp = (char*)ws.p + 4 * arr + rows;
-  hipLaunchKernelGGL(keys_kernel, dim3((batch_seq + kThreads - 1) / kThreads), dim3(kThreads), 0,
-                     s, tokens, batch_seq, vocab, keys, vals);
-  ARK_HIP(hipGetLastError());
-  ARK_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, temp, keys, skeys, vals, svals, n, 0, end_bit,
-                                             s));
+  if (block_sort) {
+    hipLaunchKernelGGL(block_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, tokens, batch_seq,
+                       vocab, end_bit, skeys, svals);
+    ARK_HIP(hipGetLastError());
+  } else {
+    hipLaunchKernelGGL(keys_kernel, dim3((batch_seq + kThreads - 1) / kThreads), dim3(kThreads),
+                       0, s, tokens, batch_seq, vocab, keys, vals);
+    ARK_HIP(hipGetLastError());
+    ARK_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, temp, keys, skeys, vals, svals, n, 0,
+                                               end_bit, s));
+  }
   const uint32_t gvec = ((d % 4u) == 0 && (((uintptr_t)dx0 & 15u) == 0)) ? 1u : 0u;
   hipLaunchKernelGGL(gather_kernel, dim3(batch_seq), dim3(kThreads), 0, s, dx0, svals, d, gvec,
                      xs);

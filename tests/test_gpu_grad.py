@@ -32,8 +32,12 @@ def _zipf_tokens(rng, n, vocab, extra=0):
 
 @pytest.mark.parametrize("vocab,d,n,extra", [(32000, 768, 4096, 0), (32000, 768, 4096, 50),
                                              (1000, 33, 777, 10), (5, 64, 2000, 2),
-                                             (32000, 768, 1, 0)])
+                                             (32000, 768, 1, 0), (32768, 768, 4096, 0),
+                                             (32000, 768, 4097, 0), (32000, 256, 9000, 5)])
 def test_scatter_matches_oracle(vocab, d, n, extra):
+    """Up to 4096 tokens the positions are sorted by one block in LDS, past
+    that by the device-wide radix sort; vocab 32768 puts the largest real key
+    on the block sort's padding key."""
     torch = _torch()
     rng = np.random.default_rng(vocab + d + n)
     tokens = _zipf_tokens(rng, n, vocab, extra)
@@ -47,6 +51,26 @@ def test_scatter_matches_oracle(vocab, d, n, extra):
     got = _bits(gg).reshape(vocab, d)
     bad = np.argwhere(got != want.view(np.uint32))
     assert bad.size == 0, f"{len(bad)} elements differ, first {bad[0].tolist()}"
+
+
+def test_scatter_largest_key_ties_with_the_block_sort_padding():
+    """vocab 32768 sorts over 15 bits, where the padding past n (all-ones key)
+    equals the largest real key 32767: the real rows of that token must still
+    come first, in order, and only they are added."""
+    torch = _torch()
+    vocab, d, n = 32768, 64, 1000
+    rng = np.random.default_rng(13)
+    tokens = rng.integers(0, vocab, n).astype(np.uint32)
+    tokens[::7] = vocab - 1
+    tokens[3] = vocab + 5  # out of range: row 0
+    dx0 = rng.standard_normal((n, d)).astype(np.float32)
+    g = rng.standard_normal((vocab, d)).astype(np.float32)
+    want = g.copy()
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.from_numpy(g).cuda()
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
 
 
 def test_scatter_one_long_run_and_order():
