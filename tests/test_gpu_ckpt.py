@@ -181,6 +181,58 @@ def test_full_eko237m_image():
             np.testing.assert_array_equal(_bits(b), _quiet16(_bits(a)))
 
 
+def test_resume_is_bit_continuous(tmp_path):
+    """Train, save (V4 with the AMP trailer), load into fresh buffers and a
+    fresh optimizer, continue: the weights, moments and scaler state equal an
+    uninterrupted run's bit for bit.  A non-finite step before the save and a
+    growth period of 3 make the skipped/clean counters and the scale part of
+    what must carry over (the reference restarts its scaler at init on every
+    resume, training.rs:120-124)."""
+    torch = _torch()
+    from ark_amd import synth
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    specs = EkoConfig(n_layers=2, d_model=64, hidden=96, vocab=500).tensors()
+    seed, scale = 5, 1024.0
+    sig = synth.log_uniform_sigmas(len(specs), seed)
+    cfg = AdamConfig(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_max=2.0 ** 24, scale_up_every=3)
+    N, M, bad = 6, 5, 2
+
+    def run(ps, opt, steps):
+        for k in steps:
+            synth.regen_grads(ps, seed, sig, scale, k)
+            if k == bad:
+                ps.g(0).view(torch.int16)[3] = 0x7C00
+            opt.step_all(cfg.lr)
+
+    pa = synth.problem(specs, seed, cfg.weight_decay, sig, scale)
+    oa = Optimizer(cfg, pa, amp)
+    run(pa, oa, range(N + M))
+
+    pb = synth.problem(specs, seed, cfg.weight_decay, sig, scale)
+    ob = Optimizer(cfg, pb, amp)
+    run(pb, ob, range(N))
+    path = str(tmp_path / "resume.ark")
+    ckpt.save_params(path, pb, ob, global_step=N)
+    ob.close()
+
+    pc = synth.problem(specs, seed + 1, cfg.weight_decay, sig, scale)  # other contents
+    oc = Optimizer(cfg, pc, amp)
+    info, st = ckpt.load_params(path, pc, oc)
+    assert info.has_amp and st.skipped_steps == 1 and info.adam_step == N - 1
+    run(pc, oc, range(N, N + M))
+    torch.cuda.synchronize()
+    sa, sc = oa.get_state(), oc.get_state()
+    for f in ("t", "loss_scale", "clean_steps", "consecutive_nonfinite", "skipped_steps"):
+        assert getattr(sa, f) == getattr(sc, f), f
+    assert sa.loss_scale != scale  # the scale moved: the trailer carried it
+    for i in range(len(specs)):
+        for a, c in ((pa.w(i), pc.w(i)), (pa.m(i), pc.m(i)), (pa.v(i), pc.v(i))):
+            it = torch.int16 if a.element_size() == 2 else torch.int32
+            assert torch.equal(a.view(it), c.view(it)), specs[i].name
+    oa.close(), oc.close()
+
+
 def test_pack_unpack_empty_and_tiny_records():
     """Empty records (they start where the next one does), runs of one- and
     few-element records, and records of hundreds of blocks, so that one
