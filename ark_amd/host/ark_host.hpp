@@ -198,6 +198,12 @@ class Optimizer {
     if ((momentos_m.size() != esperados && momentos_m.size() != esperados + 1) ||
         (momentos_v.size() != esperados && momentos_v.size() != esperados + 1))
       return false;
+    // Every exit (a false return, a throw) waits for the copies already
+    // queued from the caller's vectors.
+    struct Drain {
+      hipStream_t s;
+      ~Drain() { (void)hipStreamSynchronize(s); }
+    } drain{stream_};
     auto put = [&](size_t ti, size_t k) {
       const TensorRef& t = tensors_[ti];
       if (momentos_m[k].size() != t.n) return false;
