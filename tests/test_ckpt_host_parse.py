@@ -96,3 +96,48 @@ def test_image_bytes_matches_oracle_length(amp):
     out = C.c_uint64()
     assert lib().ark_ckpt_v4_image_bytes(recs, len(t), amp, C.byref(out)) == 0
     assert out.value == len(K.write_v4(0, 0, t)) + 40 * amp
+
+
+def _layout_fits(ci, ns, ts):
+    """The probed layout inside the file: headers plus data no longer than it."""
+    head = {4: 28, 3: 28, 2: 20}[ci.version]
+    rec = 16 if ci.version == 4 else 8
+    total = head + sum(rec + n * (2 if t == _abi.CKPT_F16 else 4) for n, t in zip(ns, ts))
+    return total <= ci.file_bytes
+
+
+@pytest.mark.parametrize("version", [4, 3, 2])
+def test_probe_survives_corrupted_and_truncated_files(tmp_path, version):
+    """Random truncations and byte overwrites of a valid file (headers, sizes,
+    types, data): the parser either rejects the file with EIO or reports a
+    layout that fits inside it -- never a crash, never an out-of-file read."""
+    from hypothesis import given, settings, HealthCheck
+    from hypothesis import strategies as st
+
+    rng = np.random.default_rng(version)
+    t = [rng.standard_normal(n).astype(np.float32) for n in (5, 1, 0, 33)]
+    if version == 4:
+        t[0] = rng.integers(0, 65536, 5, dtype=np.uint32).astype(np.uint16)
+        good = K.write_v4(7, 6, t) + K.amp_trailer(bytes(40 - 8))
+    elif version == 3:
+        good = K.write_v3(7, 6, t)
+    else:
+        good = K.write_v2(7, t)
+    p = tmp_path / f"f{version}.bin"
+
+    @settings(max_examples=300, deadline=None, suppress_health_check=list(HealthCheck))
+    @given(cut=st.integers(0, len(good)), off=st.integers(0, len(good) - 1),
+           junk=st.binary(min_size=1, max_size=12))
+    def check(cut, off, junk):
+        b = bytearray(good)
+        b[off:off + len(junk)] = junk
+        b = bytes(b[:len(b) - cut])
+        p.write_bytes(b)
+        rc, ci, ns, ts = _probe(p, max_n=8)
+        assert rc in (0, _abi.EIO)
+        if rc == 0:
+            assert ci.file_bytes == len(b)
+            if ci.n_tensors <= 8:
+                assert _layout_fits(ci, ns, ts)
+
+    check()
