@@ -368,17 +368,7 @@ std::vector<uint32_t> make_hints(const std::vector<uint32_t>& start, uint32_t nr
   return h;
 }
 
-struct StreamBuf {
-  void* p = nullptr;
-  hipStream_t s = nullptr;
-  hipError_t alloc(size_t bytes, hipStream_t stream) {
-    s = stream;
-    return hipMallocAsync(&p, bytes, stream);
-  }
-  ~StreamBuf() {
-    if (p) (void)hipFreeAsync(p, s);
-  }
-};
+using ark::StreamBuf;
 struct PinBuf {
   void* p = nullptr;
   ~PinBuf() {

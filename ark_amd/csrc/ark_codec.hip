@@ -128,10 +128,7 @@ __global__ __launch_bounds__(Shape<DIR>::kLanes) void codec_batch(
 
 constexpr uint64_t kMaxFlatBlocks = 1u << 20;
 
-bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
-  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
-  return x < y + bbytes && y < x + abytes;
-}
+using ark::overlaps;
 
 template <uint32_t DIR>
 int run_flat(const void* src, void* dst, uint64_t n, void* stream) {

@@ -51,6 +51,26 @@ struct DeviceGuard {
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// True when [a, a + abytes) and [b, b + bbytes) share a byte.
+inline bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bbytes && y < x + abytes;
+}
+
+// Scratch device memory from the stream-ordered pool, freed in stream order
+// when the owner goes out of scope (after the work queued on it).
+struct StreamBuf {
+  void* p = nullptr;
+  hipStream_t s = nullptr;
+  hipError_t alloc(size_t bytes, hipStream_t stream) {
+    s = stream;
+    return hipMallocAsync(&p, bytes, stream);
+  }
+  ~StreamBuf() {
+    if (p) (void)hipFreeAsync(p, s);
+  }
+};
+
 }  // namespace ark
 
 #define ARK_HIP(call)                                       \

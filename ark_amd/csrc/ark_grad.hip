@@ -245,22 +245,9 @@ __global__ __launch_bounds__(kTileCols) void run_kernel(float* __restrict__ g, u
 
 constexpr uint64_t kMaxFlatBlocks = 1u << 20;
 
-bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
-  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
-  return x < y + bbytes && y < x + abytes;
-}
+using ark::overlaps;
 
-struct StreamBuf {
-  void* p = nullptr;
-  hipStream_t s = nullptr;
-  hipError_t alloc(size_t bytes, hipStream_t stream) {
-    s = stream;
-    return hipMallocAsync(&p, bytes, stream);
-  }
-  ~StreamBuf() {
-    if (p) (void)hipFreeAsync(p, s);
-  }
-};
+using ark::StreamBuf;
 
 }  // namespace
 
