@@ -112,6 +112,14 @@ def check(rc):
     return rc
 
 
+def current_stream(t=None):
+    """torch's current HIP stream (of t's device when t is given), as the
+    void* the C ABI takes."""
+    import torch
+    s = torch.cuda.current_stream(t.device) if t is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
 def exported_symbols():
     """Function names declared in include/*.h (every one must be exported)."""
     import re

@@ -15,12 +15,7 @@ import os
 from dataclasses import dataclass
 
 from . import _abi
-from ._lib import check, lib
-
-
-def _stream():
-    import torch
-    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+from ._lib import check, lib, current_stream as _stream
 
 
 class Records:

@@ -9,12 +9,7 @@ ark_quant_f32_to_f16 (proyecto_ark/ark01/src/ffi.rs:87-92) as tensors, and
 import ctypes as C
 
 from . import _abi
-from ._lib import check, lib
-
-
-def _stream(t):
-    import torch
-    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+from ._lib import check, lib, current_stream as _stream
 
 
 def _flat(t, size):

@@ -9,12 +9,7 @@ bridge.m:922-928 with the loop's exact summation order.
 import ctypes as C
 
 from . import _abi
-from ._lib import check, lib
-
-
-def _stream():
-    import torch
-    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+from ._lib import check, lib, current_stream as _stream
 
 
 def _f32(t):

@@ -7,12 +7,11 @@ gradients of step k use (tensor_id = i, step = k).  The CPU oracle builds the
 same inputs from the same counter-based generator, so both sides start from
 identical bits.
 """
-import ctypes as C
 
 import numpy as np
 
 from . import _abi
-from ._lib import check, lib
+from ._lib import check, lib, current_stream as _stream
 
 WEIGHT_STEP = 0xFFFFFFFF
 W_SIGMA = 0.02   # weights ~ N(0, 0.02)
@@ -28,11 +27,6 @@ def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
     """Per-tensor sigma = 10^U(lo, hi), drawn on the host (BASELINE c2)."""
     rng = np.random.default_rng(seed)
     return [float(np.float32(10.0 ** rng.uniform(lo, hi))) for _ in range(n)]
-
-
-def _stream(t):
-    import torch
-    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
 def normal_f16(t, seed, tensor_id, step, sigma_scale):
