@@ -209,7 +209,15 @@ __global__ __launch_bounds__(kTileCols) void run_kernel(float* __restrict__ g, u
 #pragma unroll
       for (int j = 0; j < kColRows; ++j) acc = acc + v[j];
     }
-    for (; k < len; ++k) acc = acc + ld_g<float>(x + (uint64_t)k * d + c);
+    if (k < len) {  // the last len % kColRows rows, loaded together as well
+      float v[kColRows];
+#pragma unroll
+      for (int j = 0; j < kColRows; ++j)
+        if (k + j < len) v[j] = ld_g<float>(x + (uint64_t)(k + j) * d + c);
+#pragma unroll
+      for (int j = 0; j < kColRows; ++j)
+        if (k + j < len) acc = acc + v[j];
+    }
     st_g<float>(gp, acc);
     return;
   }
