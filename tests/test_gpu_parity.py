@@ -138,6 +138,24 @@ def test_ragged_and_tiny_tensors():
     opt.close()
 
 
+def test_empty_tensors_in_the_table():
+    """Zero-length tensors among others contribute nothing and are skipped;
+    a table of only empty tensors still runs the AMP state machine (norm 0,
+    the step counts as applied, as the reference's loop over empty slices)."""
+    specs = [TensorSpec("z0", (0,), True, False), TensorSpec("a", (5,), True, False),
+             TensorSpec("z1", (0,), False, True), TensorSpec("b", (4096,), True, False),
+             TensorSpec("z2", (0,), True, False)]
+    sig = [1e-3] * len(specs)
+    cfg, ps, ts, opt, ref = _make(specs, 6, sig, 512.0)
+    _run_steps(ps, ts, opt, ref, 6, sig, 512.0, 3, cfg.lr)
+    opt.close()
+    specs = [TensorSpec("z0", (0,), True, False), TensorSpec("z1", (0,), False, True)]
+    cfg, ps, ts, opt, ref = _make(specs, 6, [1e-3, 1e-3], 512.0)
+    last = _run_steps(ps, ts, opt, ref, 6, [1e-3, 1e-3], 512.0, 3, cfg.lr)
+    assert last.applied == 1 and last.grad_norm == 0.0 and last.state.t == 3
+    opt.close()
+
+
 def test_fp32_gradients():
     specs = [TensorSpec("a", (3000,), True, False), TensorSpec("b", (768,), False, True)]
     sig = [1e-3, 1e-3]
