@@ -265,6 +265,34 @@ def test_pack_unpack_empty_and_tiny_records():
         np.testing.assert_array_equal(x, y)
 
 
+def test_thousands_of_tiny_records():
+    """3000 records of 0-40 elements (fp16 and fp32, so every later record is
+    misaligned one way or another) followed by a large one: hundreds of
+    records inside one 256-block range of the kernels' tensor lookup; image
+    bytes against the oracle writer, and unpacked back."""
+    torch = _torch()
+    rng = np.random.default_rng(23)
+    sizes = [int(x) for x in rng.integers(0, 41, 3000)] + [300000]
+    tens = [torch.empty(n, dtype=torch.float16 if rng.random() < 0.5 else torch.float32,
+                        device="cuda") for n in sizes]
+    _fill_random(tens, 24)
+    img = torch.empty(ckpt.image_bytes(tens), dtype=torch.uint8, device="cuda")
+    ckpt.pack(tens, img, 5, 4)
+    torch.cuda.synchronize()
+    want = K.write_v4(5, 4, [_bits(t) if t.numel() else
+                             np.zeros(0, np.uint16 if t.element_size() == 2 else np.float32)
+                             for t in tens])
+    assert img.cpu().numpy().tobytes() == want
+    back = [torch.empty_like(t) for t in tens]
+    ckpt.unpack(img, back)
+    torch.cuda.synchronize()
+    for a, b in zip(tens, back):
+        x, y = _bits(a), _bits(b)
+        if a.element_size() == 2:
+            x = _quiet16(x)
+        np.testing.assert_array_equal(x, y)
+
+
 def test_rejects_bad_files(tmp_path):
     torch = _torch()
     x = [torch.zeros(5, dtype=torch.float16, device="cuda"),

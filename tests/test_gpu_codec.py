@@ -133,3 +133,31 @@ def test_rejects_bad_buffers():
         check(lib().ark_hip_quant_f32_to_f16(h.ctypes.data, y.data_ptr(), 16, None))
     with pytest.raises(ArkOptError, match="overlap"):
         check(lib().ark_hip_dequant_f16_to_f32(x.data_ptr(), x.data_ptr() + 4, 4, None))
+
+
+def test_plans_over_thousands_of_tiny_spans():
+    """2000 spans of 0-300 elements (empty ones skipped) in one codec plan
+    and one accumulation plan, against the oracle's conversion and an fp32
+    add: every segment ragged, a 2000-entry descriptor table."""
+    torch = _torch()
+    from ark_amd import grad
+    rng = np.random.default_rng(21)
+    sizes = [int(x) for x in rng.integers(0, 301, 2000)]
+    h16 = [rng.integers(0, 65536, n, dtype=np.uint32).astype(np.uint16) for n in sizes]
+    src = [torch.from_numpy(h.view(np.int16)).cuda().view(torch.float16) for h in h16]
+    dst = [torch.empty(n, dtype=torch.float32, device="cuda") for n in sizes]
+    plan = codec.CodecPlan(list(zip(src, dst)), "f16_to_f32")
+    plan.run()
+    torch.cuda.synchronize()
+    for h, d in zip(h16, dst):
+        want = oracle.f16_to_f32(h) if h.size else np.zeros(0, np.float32)
+        assert np.array_equal(d.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    plan.close()
+    a = [torch.randn(n, device="cuda") for n in sizes]
+    b = [torch.randn(n, device="cuda") for n in sizes]
+    want = [x + y for x, y in zip(a, b)]
+    gp = grad.GradPlan(list(zip(a, b)))
+    gp.run()
+    torch.cuda.synchronize()
+    assert all(torch.equal(x.view(torch.int32), w.view(torch.int32)) for x, w in zip(a, want))
+    gp.close()
