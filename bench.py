@@ -25,8 +25,16 @@ sys.path.insert(0, ROOT)
 
 METRIC = "EKO-237M fused AdamW step ms + achieved HBM GB/s vs peak (1 GPU)"
 PEAK_HBM_GBS = 8000.0
-BYTES_STEP = 24  # pass 1 reads g (2 B); the fused update reads g,w,m,v and writes w,m,v (22 B)
-BYTES_ADAMW = 22
+
+
+def step_bytes(grad):
+    """Algorithmic bytes per parameter of the step and of its AdamW pass: the
+    norm pass reads g, the fused update reads g, w, m, v and writes w, m, v
+    (g 2 B fp16 / 4 B fp32, w 2+2, m 4+4, v 4+4): 24 and 22 B for fp16
+    gradients, 28 and 24 B for fp32."""
+    gs = 2 if grad == "f16" else 4
+    return 2 * gs + 20, gs + 20
+
 
 WORKLOADS = {
     "c2": dict(desc="EKO-237M: 30 layers, d 768, ffn 2048, tied embed 32000x768 (272 tensors)",
@@ -52,19 +60,19 @@ def sigmas_for(name, specs):
     return [w["sigma"]] * len(specs)
 
 
-def run_gpu(name, steps, warmup):
+def run_gpu(name, steps, warmup, grad="f16"):
     import torch
     torch.cuda.set_device(0)
     # everything on one non-default stream, so the step can also be captured
     # in a HIP graph
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        return _run_gpu(name, steps, warmup, stream)
+        return _run_gpu(name, steps, warmup, stream, grad)
 
 
-def _run_gpu(name, steps, warmup, stream):
+def _run_gpu(name, steps, warmup, stream, grad="f16"):
     import torch
-    from ark_amd import synth
+    from ark_amd import _abi, synth
     from ark_amd.eko import config_tensors
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
 
@@ -74,7 +82,8 @@ def _run_gpu(name, steps, warmup, stream):
     cfg = AdamConfig(**HP)
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
-    ps = synth.problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
+    gdt = _abi.GRAD_F16 if grad == "f16" else _abi.GRAD_F32
+    ps = synth.problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"], grad_dtype=gdt)
     opt = Optimizer(cfg, ps, amp)
     torch.cuda.synchronize()
     _, info = opt.step_all(cfg.lr, info=True)
@@ -143,12 +152,13 @@ def calib_copy(nbytes=1 << 30, reps=3):
     log(f"[bench] calibration copy: {reps} x {nbytes} bytes")
 
 
-def run_cpu_baseline(name, budget_s, threads):
+def run_cpu_baseline(name, budget_s, threads, grad="f16"):
     """The C oracle (same arithmetic, bit-identical results) timed on the
     host cores: full steps of the same workload until budget_s is spent."""
     import numpy as np
     import oracle
     from oracle import harness as H
+    from ark_amd import _abi
     from ark_amd.eko import config_tensors
     from ark_amd.optimizer import AdamConfig, AmpConfig, hparams
 
@@ -157,8 +167,9 @@ def run_cpu_baseline(name, budget_s, threads):
     sig = sigmas_for(name, specs)
     cfg = AdamConfig(**HP)
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
-    ts = H.host_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"])
-    ref = oracle.Optimizer(ts, hparams(cfg, amp), nthreads=threads)
+    gdt = _abi.GRAD_F16 if grad == "f16" else _abi.GRAD_F32
+    ts = H.host_problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"], grad_dtype=gdt)
+    ref = oracle.Optimizer(ts, hparams(cfg, amp, gdt), nthreads=threads)
     n = sum(s.n for s in specs)
     vec = oracle.set_vector(True)  # the 8-wide AVX2/F16C loops (same bits as the scalar form)
     ref.step(cfg.lr)  # warm (page in)
@@ -179,7 +190,7 @@ def run_cpu_baseline(name, budget_s, threads):
                 break
     except OSError:
         pass
-    return dict(value=round(BYTES_STEP * n / s_step / 1e9, 3), unit="GB/s", cores=threads,
+    return dict(value=round(step_bytes(grad)[0] * n / s_step / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port", ms_per_step=round(s_step * 1e3, 3),
                 sample=f"{done} full {name} steps ({n} params) in {el:.1f} s on {threads} "
                        f"threads of {os.cpu_count()} ({cpu}), "
@@ -538,6 +549,9 @@ def main():
                     help="step: the optimizer step (headline); codec: the weight codec; "
                          "ckpt: the V4 checkpoint image; grad: the gradient hand-off; "
                          "dropin: the reference's 272 single-tensor calls per step")
+    ap.add_argument("--grad", default="f16", choices=["f16", "f32"],
+                    help="step: gradient type handed to the step (f16 loss-scaled, as BASELINE's "
+                         "configs; f32, as the gradient hand-off produces)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -551,18 +565,19 @@ def main():
             calib_copy()
         return
 
-    r = run_gpu(a.workload, a.steps, a.warmup)
+    r = run_gpu(a.workload, a.steps, a.warmup, a.grad)
     if a.calib_copy:
         calib_copy()
     n = r["n_params"]
-    gbs = BYTES_STEP * n / (r["ms_step"] * 1e-3) / 1e9
-    adam_gbs = BYTES_ADAMW * n / (r["ms_adamw"] * 1e-3) / 1e9
-    traffic, tsrc = traffic_from_profiles(a.workload)
+    b_step, b_adamw = step_bytes(a.grad)
+    gbs = b_step * n / (r["ms_step"] * 1e-3) / 1e9
+    adam_gbs = b_adamw * n / (r["ms_adamw"] * 1e-3) / 1e9
+    traffic, tsrc = traffic_from_profiles(a.workload) if a.grad == "f16" else (None, None)
     cpu = None
     if not a.no_cpu:
         th = a.cpu_threads or min(16, os.cpu_count() or 1)
         log(f"[bench] cpu baseline: {th} threads, ~{a.cpu_seconds}s")
-        cpu = run_cpu_baseline(a.workload, a.cpu_seconds, th)
+        cpu = run_cpu_baseline(a.workload, a.cpu_seconds, th, a.grad)
     out = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -580,8 +595,8 @@ def main():
             "workload": f"{a.workload}: {WORKLOADS[a.workload]['desc']}",
             "params": n,
             "tensors": r["n_tensors"],
-            "storage": "w fp16, g fp16 (loss-scaled), m/v fp32",
-            "bytes_per_step": BYTES_STEP * n,
+            "storage": f"w fp16, g {a.grad} (loss-scaled), m/v fp32",
+            "bytes_per_step": b_step * n,
             "hparams": HP,
             "loss_scale": WORKLOADS[a.workload]["loss_scale"],
             "clipped": r["clipped"],
@@ -600,7 +615,7 @@ def main():
             "frac": round(adam_gbs / PEAK_HBM_GBS, 4),
             "traffic": traffic,
             "traffic_source": tsrc,
-            "algorithmic_bytes_per_launch": BYTES_ADAMW * n,
+            "algorithmic_bytes_per_launch": b_adamw * n,
         },
         "cpu_baseline": cpu,
     }
