@@ -53,14 +53,15 @@ constexpr int kThreads = 256;  // header and check kernels
 constexpr uint32_t kHintShift = 8;  // pack/unpack blocks per find_rec hint: 256
 // Pack and unpack launch shapes: lanes per block, and 16-byte image chunks
 // (pack) or units (unpack) per lane, kLanes * 16 bytes apart.  Measured on
-// MI355X over the EKO-237M image: 256 lanes with one chunk per lane beat 64,
-// 128 and 512 lanes with one, two or four per lane (pack 0.91 ms against
-// 0.96-1.09 ms per call, unpack 0.94 against 0.95-0.99 ms).
+// MI355X over the EKO-237M image (per call): pack is best at 256 lanes with
+// one chunk per lane (0.87 ms; 64-512 lanes with one to four chunks
+// 0.86-1.05 ms), unpack at 512 lanes with two units per lane (0.83 ms against
+// 0.85 ms for 256 x 1 and up to 0.89 ms for the others).
 constexpr int kPackLanes = 256;
 constexpr int kPackChunks = 1;
 constexpr uint32_t kPackSegBytes = 16u * kPackLanes * kPackChunks;  // image bytes per block
-constexpr int kUnpackLanes = 256;
-constexpr int kUnpackUnits = 1;
+constexpr int kUnpackLanes = 512;
+constexpr int kUnpackUnits = 2;
 // elements per unpack block: kUnpackUnits 16-byte units of the file type per lane
 constexpr uint32_t unpack_seg(uint32_t ftype) {
   return (ftype == ARK_CKPT_F16 ? 8u : 4u) * kUnpackLanes * kUnpackUnits;
