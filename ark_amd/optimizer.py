@@ -20,7 +20,6 @@ import numpy as np
 
 from . import _abi
 from ._lib import check, lib
-from .eko import TensorSpec
 
 
 @dataclass

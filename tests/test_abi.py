@@ -5,9 +5,6 @@ import ctypes as C
 import os
 import re
 
-import numpy as np
-import pytest
-
 from ark_amd import _abi
 from ark_amd import _lib
 

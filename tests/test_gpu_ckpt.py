@@ -4,9 +4,6 @@ written from device buffers equal the oracle's bytes, files the oracle
 writes (V4, V3, V2) load into device buffers as the reference's chain of
 conversions would, and the full EKO-237M image packs and unpacks bit for
 bit."""
-import ctypes as C
-import os
-
 import numpy as np
 import pytest
 

@@ -3,7 +3,6 @@ stepped in an interleaved order with no host wait between them (so their
 kernels may overlap on the device), each give exactly the oracle's result
 for their own problem.  Also a codec plan and a gradient plan running on a
 third stream meanwhile."""
-import numpy as np
 import pytest
 
 import oracle

@@ -4,7 +4,6 @@ stream (no host wait, no memset, no allocation), so a caller can capture it
 once and replay it.  Every replay is checked against an eager step of an
 identical problem, with eager work (new gradients, a state read) between
 replays, including a replay that must skip on a non-finite gradient."""
-import numpy as np
 import pytest
 
 from oracle import harness as H

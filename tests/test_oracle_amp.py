@@ -6,7 +6,6 @@ import json
 import os
 
 import numpy as np
-import pytest
 
 import oracle
 from ark_amd import _abi

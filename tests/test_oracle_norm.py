@@ -9,7 +9,6 @@ of the tree, exact special cases and invariants."""
 import math
 
 import numpy as np
-import pytest
 
 import oracle
 from ark_amd import _abi

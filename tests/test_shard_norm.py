@@ -6,7 +6,6 @@ on every rank, reproduces the single-device sum bit for bit, and a
 non-finite gradient on any rank turns every rank's sum into NaN.  Checked
 here with the CPU oracle standing in for each rank's norm pass, on 2 and 4
 gloo ranks (one process each, 127.0.0.1)."""
-import os
 import socket
 
 import numpy as np
