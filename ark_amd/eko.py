@@ -58,7 +58,7 @@ class EkoConfig:
         return sum(t.n for t in self.tensors(**kw))
 
 
-# BASELINE configs (see the repository's BASELINE.json):
+# The benchmark configurations:
 #   c0: one 768x768 tensor; c1: one EKO layer (9 tensors, no embedding,
 #   no gamma_final); c2/c3: EKO-237M (272 tensors); c4: 1.3B scale-up.
 EKO_LAYER = EkoConfig(n_layers=1, d_model=768, hidden=2048, vocab=32000)
@@ -67,7 +67,7 @@ EKO_1P3B = EkoConfig(n_layers=24, d_model=2048, hidden=5504, vocab=32000, n_head
 
 
 def config_tensors(name):
-    """TensorSpec list of a BASELINE config name: c0, c1, c2, c3, c4."""
+    """TensorSpec list of a benchmark configuration: c0, c1, c2, c3, c4."""
     if name == "c0":
         return [TensorSpec("w", (768, 768), True, False)]
     if name == "c1":

@@ -1,6 +1,6 @@
 """Seeded synthetic inputs on the device (include/ark_synth.h) for torch
 tensors: fp16 weights and loss-scaled fp16 gradients of the EKO shapes, and
-the parameter sets built from them (BASELINE's synthetic workloads).
+the parameter sets built from them (the benchmark configurations' workloads).
 
 Streams of the generator: weights use (tensor_id = i, step = WEIGHT_STEP);
 gradients of step k use (tensor_id = i, step = k).  The CPU oracle builds the
@@ -24,7 +24,7 @@ def grad_sigma_scale(sigma, loss_scale):
 
 
 def log_uniform_sigmas(n, seed, lo=-5.0, hi=-2.0):
-    """Per-tensor sigma = 10^U(lo, hi), drawn on the host (BASELINE c2)."""
+    """Per-tensor sigma = 10^U(lo, hi), drawn on the host (configuration c2)."""
     rng = np.random.default_rng(seed)
     return [float(np.float32(10.0 ** rng.uniform(lo, hi))) for _ in range(n)]
 

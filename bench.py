@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the fused optimizer step on one MI355X.
 
-Default workload: BASELINE config 2, the full EKO-237M parameter set (272
+Default workload: configuration c2, the full EKO-237M parameter set (272
 tensors, 236,959,488 params): fp16 weights ~N(0,0.02) (gains 1.0), fp16
 gradients N(0, sigma_t) * 65536 with per-tensor sigma_t = 10^U(-5,-2), fp32
 m/v, one fused unscale + finite check + norm + clip + AdamW + loss-scale step
@@ -550,8 +550,8 @@ def main():
                          "ckpt: the V4 checkpoint image; grad: the gradient hand-off; "
                          "dropin: the reference's 272 single-tensor calls per step")
     ap.add_argument("--grad", default="f16", choices=["f16", "f32"],
-                    help="step: gradient type handed to the step (f16 loss-scaled, as BASELINE's "
-                         "configs; f32, as the gradient hand-off produces)")
+                    help="step: gradient type handed to the step (f16 loss-scaled, as the benchmark "
+                         "configurations; f32, as the gradient hand-off produces)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()

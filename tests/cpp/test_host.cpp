@@ -177,7 +177,7 @@ int main() {
   Set d;
   Host h;
   make(sp, d, h);
-  AdamConfig cfg;  // AdamConfig::default, with the BASELINE overrides
+  AdamConfig cfg;  // AdamConfig::default, with the benchmark configurations' overrides
   cfg.beta2 = 0.95f;
   cfg.weight_decay = 0.1f;
   cfg.warmup_steps = 5;

@@ -1,5 +1,5 @@
 """Write tests/golden/oracle_steps.json: per-step scalars and SHA-256 digests
-of w, m, v produced by the CPU oracle for BASELINE configs 0 and 1 (seeded
+of w, m, v produced by the CPU oracle for configurations c0 and c1 (seeded
 synthetic inputs from the counter-based generator).  The CPU test
 regenerates them to catch oracle regressions; the GPU test compares the HIP
 path's arrays against the same digests.

@@ -1,6 +1,6 @@
 """GPU parity: the HIP path through the C ABI against the CPU oracle, bit for
-bit (scalars of every step, every w/m/v element), at BASELINE configs 0 and
-1 and at edge cases of the reference kernel (opti.s:192-360) and the AMP
+bit (scalars of every step, every w/m/v element), at configurations c0 and
+c1 and at edge cases of the reference kernel (opti.s:192-360) and the AMP
 state machine (training.rs:289-326)."""
 import ctypes as C
 
@@ -86,7 +86,7 @@ def test_calibration_copy_kernel():
 
 
 def test_config0_ten_steps_bit_exact():
-    """BASELINE c0: one 768x768 tensor, grads N(0,1e-3)*1024 fresh per step,
+    """Configuration c0: one 768x768 tensor, grads N(0,1e-3)*1024 fresh per step,
     10 steps; norm ~0.77 so no clipping."""
     specs = config_tensors("c0")
     sig = [1e-3]
@@ -97,7 +97,7 @@ def test_config0_ten_steps_bit_exact():
 
 
 def test_config1_layer_hundred_steps_bit_exact():
-    """BASELINE c1: one EKO layer (9 tensors, g1/g2 = 1.0 without wd), 100
+    """Configuration c1: one EKO layer (9 tensors, g1/g2 = 1.0 without wd), 100
     steps; norm ~2.66 so every step clips."""
     specs = config_tensors("c1")
     sig = [1e-3] * len(specs)

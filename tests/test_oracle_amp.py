@@ -60,7 +60,7 @@ def test_cap_resets_counter_and_never_exceeds_max():
 
 
 def test_config3_start_above_default_cap_never_grows():
-    """BASELINE c3 starts at 65536 > the default cap 8192: min(2S, max) < S,
+    """Configuration c3 starts at 65536 > the default cap 8192: min(2S, max) < S,
     so the scale never grows (Q3) until loss_scale_max is raised."""
     hp = _hp(loss_scale_init=65536.0)
     st = _state(hp)
