@@ -1,8 +1,7 @@
 """GPU parity at the benchmark configurations' full sizes: the EKO-237M set
 (c2), its 5000-step AMP stress trajectory (c3) and the 1.3B scale-up (c4),
-checked against the
-CPU oracle bit for bit (every scalar and every w/m/v element of the steps
-run), plus the state/restore and timing entry points."""
+checked against the CPU oracle bit for bit (every scalar and every w/m/v
+element of the steps run), plus the state/restore and timing entry points."""
 import os
 
 import numpy as np
