@@ -381,6 +381,39 @@ def test_clip_boundary_matches_oracle(true_grads, clipped):
     opt.close()
 
 
+def test_element_math_over_an_edge_value_grid():
+    """Every combination of edge values of w, g, m and v (signed zeros,
+    subnormals, fp16 max, huge and tiny moments, infinite and NaN state,
+    a negative v whose square root is NaN) in one tensor, one step without
+    unscale or clip: each element against the oracle's opti.s:278-308
+    sequence (NaNs compared as NaNs)."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    f16 = lambda xs: np.array(xs, np.float16).view(np.uint16)
+    ws = np.concatenate([f16([0.0, -0.0, 6e-8, 1e-3, 1.0, -1.0, 65504.0, -65504.0]),
+                         np.array([0x7C00, 0x7E00], np.uint16)])
+    gs = f16([0.0, -0.0, 6e-8, -6e-8, 1e-3, -1.0, 1.0, 100.0, -1000.0, 60000.0])
+    ms = np.array([0.0, -0.0, 1e-30, -1e-3, 1.0, 1e30, np.inf, -np.inf, np.nan], np.float32)
+    vs = np.array([0.0, 1e-45, 1e-30, 1e-8, 1.0, 1e30, 3e38, np.inf, np.nan, -1.0], np.float32)
+    W, G, M, V = (a.ravel() for a in np.meshgrid(ws, gs, ms, vs, indexing="ij"))
+    n = W.size
+    cfg = AdamConfig(lr=1e-2, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1e30)
+    ps = ParamSet([TensorSpec("grid", (n,), True, False)], cfg.weight_decay)
+    ps.w(0).copy_(torch.from_numpy(W.view(np.int16)).view(torch.float16))
+    ps.g(0).copy_(torch.from_numpy(G.view(np.int16)).view(torch.float16))
+    ps.m(0).copy_(torch.from_numpy(M.copy()))
+    ps.v(0).copy_(torch.from_numpy(V.copy()))
+    ts = [oracle.HostTensor(W.copy(), G.copy(), M.copy(), V.copy(), cfg.weight_decay)]
+    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=1.0))
+    ref = oracle.Optimizer(ts, opt.hp)
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert gi.applied == 1 and not H.info_matches(gi, ri)
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0, c
+    opt.close()
+
+
 def test_edge_values_weights_near_overflow_and_subnormal_grads():
     """Weights near 65504 (overflow to inf on requantisation), fp16
     subnormal weights and gradients, zero gradients."""
