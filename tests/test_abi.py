@@ -135,3 +135,28 @@ def test_next_rows_reject_bad_arguments_before_device_calls():
     assert L.ark_ckpt_v4_image_bytes(recs, 1, 0, C.byref(out)) == _abi.EINVAL and "dtype" in msg()
     assert L.ark_ckpt_save_v4(None, 0, 0, recs, 1, None, None) == _abi.EINVAL
     assert L.ark_ckpt_probe(None, None, None, None, 0) == _abi.EINVAL
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No fallback path: with the library absent, the loader and the entry
+    points above it raise, naming the missing file (run in a fresh process so
+    this process's loaded library is untouched)."""
+    import subprocess
+    import sys
+    missing = str(tmp_path / "libark_opt.so")
+    code = (
+        "import sys\n"
+        "from ark_amd import _lib, ckpt\n"
+        "_lib.LIB_PATH = sys.argv[1]\n"
+        "_lib._lib = None\n"
+        "for f in (_lib.lib, lambda: ckpt.probe(sys.argv[1]), lambda: _lib.check(-1)):\n"
+        "    try:\n"
+        "        f()\n"
+        "    except ImportError as e:\n"
+        "        assert sys.argv[1] in str(e), e\n"
+        "    else:\n"
+        "        raise SystemExit('no error')\n"
+        "print('ok')\n")
+    r = subprocess.run([sys.executable, "-c", code, missing], cwd=ROOT, capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
