@@ -113,6 +113,35 @@ def test_scatter_run_lengths_at_the_path_boundaries(d):
     np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("d,g_off", [(768, 0), (4, 0), (68, 0), (100, 0), (1028, 0), (768, 1)])
+def test_scatter_long_runs_at_odd_widths(d, g_off):
+    """Runs of 127 to 1500 rows (many 60-row rounds, then a tail) at widths
+    that leave a partial column tile (4, 68, 100, 1028), and with an
+    embedding gradient that is only 4-byte aligned (g_off = 1); the
+    order-revealing values (1e8, 1, -1e8, 1) straddle rows 510-513 of the
+    1500-row run."""
+    torch = _torch()
+    rng = np.random.default_rng(100 + d + g_off)
+    lengths = [127, 128, 129, 255, 256, 257, 511, 512, 513, 1024, 1025, 1500, 3]
+    vocab = 2000
+    ids = rng.choice(vocab, len(lengths), replace=False)
+    tokens = np.concatenate([np.full(k, t, np.uint32) for k, t in zip(lengths, ids)])
+    tokens = tokens[rng.permutation(len(tokens))]
+    n = len(tokens)
+    dx0 = (rng.standard_normal((n, d)) * 10.0 ** rng.integers(-4, 4, (n, 1))).astype(np.float32)
+    rows = np.flatnonzero(tokens == ids[lengths.index(1500)])
+    dx0[rows[510:514], :] = np.array([1e8, 1.0, -1e8, 1.0], np.float32)[:, None]
+    g = rng.standard_normal((vocab, d)).astype(np.float32)
+    want = g.copy()
+    oracle.embed_scatter(want, tokens, dx0)
+    base = torch.zeros(vocab * d + g_off, device="cuda")
+    gg = base[g_off:].view(vocab, d)
+    gg.copy_(torch.from_numpy(g))
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
 def test_scatter_unaligned_rows_take_the_scalar_path():
     torch = _torch()
     vocab, d, n = 300, 64, 500
