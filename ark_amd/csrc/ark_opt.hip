@@ -158,6 +158,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
     if (t.n == 0) continue;
+    if (t.n > (1ull << 48)) return fail(ARK_OPT_EINVAL, "tensor %d: n too large", i);
     if (((uintptr_t)t.w & 1u) || ((uintptr_t)t.g & (gsz - 1)) ||
         ((uintptr_t)t.m & 3u) || ((uintptr_t)t.v & 3u))
       return fail(ARK_OPT_EINVAL, "tensor %d: pointer not aligned to its element", i);
@@ -411,7 +412,7 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   if (n == 0) return ARK_OPT_OK;
   if (((uintptr_t)w & 1u) || ((uintptr_t)g & 3u) || ((uintptr_t)m & 3u) || ((uintptr_t)v & 3u))
     return fail(ARK_OPT_EINVAL, "pointer not aligned to its element");
-  if ((n + ark::kRow - 1) / ark::kRow * 64u >= (1ull << 32))
+  if (n > (1ull << 48) || (n + ark::kRow - 1) / ark::kRow * 64u >= (1ull << 32))
     return fail(ARK_OPT_EINVAL, "n too large (%llu)", (unsigned long long)n);
   int rc;
   if ((rc = check_buffer(w, n * 2u, "w", 0))) return rc;

@@ -74,6 +74,11 @@ def test_create_rejects_bad_arguments_before_device_calls():
     t[0].weight_decay = float("nan")
     rc, h, msg = _create(t, 1, _hp())
     assert rc == _abi.EINVAL and "weight_decay" in msg
+    t[0].weight_decay = 0.0
+    for n in (2 ** 64 - 1, 2 ** 63, 2 ** 48 + 1):  # segment count and byte sizes would wrap
+        t[0].n = n
+        rc, h, msg = _create(t, 1, _hp())
+        assert rc == _abi.EINVAL and "too large" in msg, (n, msg)
 
 
 def test_single_tensor_dropin_argument_checks():
@@ -86,6 +91,10 @@ def test_single_tensor_dropin_argument_checks():
     rc = L.ark_hip_adam_step_f16(0x1000, 0x2002, 0x3000, 0x4000, 10, 3e-4, 0.9, 0.999, 1e-8,
                                  0.01, 1, None)
     assert rc == _abi.EINVAL
+    for n in (2 ** 64 - 1, 2 ** 64 - 100, 2 ** 48 + 1):  # the grid-size test would wrap
+        rc = L.ark_hip_adam_step_f16(0x1000, 0x2000, 0x3000, 0x4000, n, 3e-4, 0.9, 0.999, 1e-8,
+                                     0.01, 1, None)
+        assert rc == _abi.EINVAL and "too large" in L.ark_opt_last_error().decode(), n
 
 
 def test_synth_argument_checks():
