@@ -188,11 +188,11 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   }
   const uint64_t nseg = segs.size();
   int spb = ark::sumsq_spb(nseg);
-  // ARK_OPT_SUMSQ_SPB=8|16|32|64 overrides the segments per norm block (a
+  // ARK_OPT_SUMSQ_SPB=1|2|4|...|64 overrides the segments per norm block (a
   // tuning knob; the canonical tree makes the result independent of it).
   if (const char* env = getenv("ARK_OPT_SUMSQ_SPB")) {
     const int v = atoi(env);
-    if ((v == 8 || v == 16 || v == 32 || v == 64) && (nseg + v - 1) / v <= ark::kMaxParts)
+    if (v >= 1 && v <= 64 && (v & (v - 1)) == 0 && (nseg + v - 1) / v <= ark::kMaxParts)
       spb = v;
   }
   const uint64_t parts = (nseg + spb - 1) / spb;

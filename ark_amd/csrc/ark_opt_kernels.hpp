@@ -96,7 +96,8 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
-// Segments per sumsq block (8; 16, 32 or 64 only past kMaxParts partials).
+// Segments per sumsq block: 8; 16, 32 or 64 only past kMaxParts partials;
+// 4, 2 or 1 while fewer than 512 blocks would cover the table.
 int sumsq_spb(uint64_t nseg);
 constexpr uint32_t kMaxParts = 64u * kFinThreads;  // partial-buffer capacity
 // Above kFinTarget partials, fold_kernel first reduces aligned groups of
