@@ -616,7 +616,7 @@ int pwrite_all(int fd, const void* buf, uint64_t len, uint64_t off, const char* 
 // One staging chunk to or from the file, split over up to kIoThreads
 // threads (the single-threaded copy between the page cache and a pinned
 // buffer, not the GPU, bounds a checkpoint's save and load).
-constexpr int kIoThreads = 8;
+constexpr int kIoThreads = 16;
 constexpr uint64_t kIoPiece = (uint64_t)4 << 20;  // at least 4 MiB per thread
 
 // memcpy split over up to kIoThreads threads (into a mapped file: the page
