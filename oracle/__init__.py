@@ -19,7 +19,9 @@ import numpy as np
 from ark_amd import _abi
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_build", "libark_oracle.so")
+# ARK_ORACLE_LIB names another build of ark_oracle.c to load instead (the
+# mutant builds of tests/test_oracle_mutants.py); it must exist.
+LIB_PATH = os.environ.get("ARK_ORACLE_LIB") or os.path.join(_HERE, "_build", "libark_oracle.so")
 
 _lib = None
 

@@ -1,0 +1,120 @@
+"""The oracle's pins catch plausible mistakes.  Each mutant is a copy of
+oracle/ark_oracle.c with one planted error -- a swapped or dropped operand, a
+wrong sign, comparison, constant or index, a rounding shortcut -- compiled on
+the CPU with the oracle's own flags.  The pin tests named beside it must fail
+against that build.  Those pins are the independent checks: the second
+restatement in Python with an exact-rational fma, closed forms, exhaustive
+conversions against F16C and numpy, brute force on small inputs, and the
+reference's own loss-scale trajectory.  Self-consistency checks (the
+vectorised loops against the scalar ones, fixtures the oracle wrote) are not
+run here.  An unmutated copy built the same way must pass them."""
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "oracle", "ark_oracle.c")
+CFLAGS = ["-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-math-errno", "-mfma",
+          "-mf16c", "-mavx2", "-pthread", "-shared"]
+
+# name: (text in ark_oracle.c, planted replacement, pin files tests/test_oracle_<x>.py)
+MUTANTS = {
+    # AdamW element update and prologue (opti.s:210-308)
+    "first_moment_takes_beta2": ("float mm = *m * beta1;", "float mm = *m * beta2;", ["adam"]),
+    "second_moment_drops_the_square": ("vv = fmaf(s->c2, gg, vv);", "vv = fmaf(s->c2, g, vv);",
+                                       ["adam"]),
+    "first_moment_not_fused": ("mm = fmaf(s->c1, g, mm);", "mm = s->c1 * g + mm;", ["adam"]),
+    "eps_inside_the_root": ("d = d + eps;", "d = sqrtf(vv + eps);", ["adam"]),
+    "update_not_scaled": ("u = u * s->lr_eff;", "u = u * s->c1;", ["adam"]),
+    "decay_sign": ("out->decay = 1.0f - lw;", "out->decay = 1.0f + lw;", ["adam"]),
+    "bias_correction_without_root": ("float r = sqrtf(out->bc2);", "float r = out->bc2;",
+                                     ["adam"]),
+    "t0_not_coerced": ("if (t == 0) t = 1;", "if (t == 0) t = 0;", ["adam"]),
+    "power_multiplies_beta": ("if (k & 1u) res = res * base;", "if (k & 1u) res = res * beta;",
+                              ["adam"]),
+    # norm and finite flag (optimizer.rs:127-145, training.rs:291)
+    "norm_not_unscaled": ("float gu = grad_f32(T->g, c->dtype, st + j) * inv_t;",
+                          "float gu = grad_f32(T->g, c->dtype, st + j);", ["norm"]),
+    "tree_pairs_strided": ("for (uint64_t i = 0; i < w; ++i) b[i] = b[2 * i] + b[2 * i + 1];",
+                           "for (uint64_t i = 0; i < w; ++i) b[i] = b[i] + b[i + w];", ["norm"]),
+    "finite_flag_misses_infinity": ("return (((const uint16_t *)g)[i] & 0x7C00u) == 0x7C00u;",
+                                    "return (((const uint16_t *)g)[i] & 0x7E00u) == 0x7E00u;",
+                                    ["norm"]),
+    # clip (optimizer.rs:145-165)
+    "clip_at_equality": ("int clipped = (norm > hp->grad_clip) && (norm > 0.0f);",
+                         "int clipped = (norm >= hp->grad_clip) && (norm > 0.0f);", ["clip"]),
+    "clip_coefficient_inverted": ("float coef = clipped ? hp->grad_clip / norm : 1.0f;",
+                                  "float coef = clipped ? norm / hp->grad_clip : 1.0f;", ["clip"]),
+    # AMP state machine (training.rs:293-326)
+    "skip_does_not_halve": ("float s = st->loss_scale * 0.5f;", "float s = st->loss_scale;",
+                            ["amp"]),
+    "growth_one_step_late": ("if (st->clean_steps >= hp->scale_up_every) {",
+                             "if (st->clean_steps > hp->scale_up_every) {", ["amp"]),
+    "capped_growth_keeps_counting": ("    st->clean_steps = 0;                                   /* :325 */",
+                                     "    if (nueva > scale) st->clean_steps = 0;", ["amp"]),
+    "early_stop_at_200": ("if (st->consecutive_nonfinite > hp->max_consecutive_nonfinite) {",
+                          "if (st->consecutive_nonfinite >= hp->max_consecutive_nonfinite) {",
+                          ["amp"]),
+    # fp16 conversions (opti.s:279, :307)
+    "narrowing_ties_round_down": ("if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;",
+                                  "if (rem > 0x1000u) h += 1u;", ["fp16"]),
+    "widening_subnormal_unit": ("float mag = (float)mant * 5.9604644775390625e-08f;",
+                                "float mag = (float)mant * 1.1920928955078125e-07f;", ["fp16"]),
+    # gradient hand-off (bridge.m:922-928)
+    "out_of_range_token_to_last_row": ("uint32_t t = (tokens[i] < vocab) ? tokens[i] : 0;",
+                                       "uint32_t t = (tokens[i] < vocab) ? tokens[i] : vocab - 1;",
+                                       ["grad"]),
+    "scatter_in_reverse": ("for (uint32_t i = 0; i < batch_seq; ++i) {",
+                           "for (uint32_t i = batch_seq; i-- > 0;) {", ["grad"]),
+}
+PINS = sorted({f for _, _, files in MUTANTS.values() for f in files})
+
+
+def _build_and_run(tmp, name, old, new, files):
+    """Build ark_oracle.c with `old` replaced by `new` (None: unchanged) and
+    run the pin files against it; returns (pytest exit code, output tail)."""
+    src = open(SRC).read()
+    if old is not None:
+        assert src.count(old) == 1, f"{name}: the text to mutate is not in ark_oracle.c once"
+        src = src.replace(old, new)
+    d = os.path.join(tmp, name)
+    os.makedirs(os.path.join(d, "oracle"))
+    os.symlink(os.path.join(ROOT, "include"), os.path.join(d, "include"))
+    shutil.copy(os.path.join(ROOT, "oracle", "ark_oracle.h"), os.path.join(d, "oracle"))
+    with open(os.path.join(d, "oracle", "ark_oracle.c"), "w") as f:
+        f.write(src)
+    so = os.path.join(d, "libark_oracle.so")
+    cc = subprocess.run(["gcc", *CFLAGS, "-o", so, os.path.join(d, "oracle", "ark_oracle.c"),
+                         "-lm"], capture_output=True, text=True)
+    assert cc.returncode == 0, f"{name}: build failed\n{cc.stderr[-2000:]}"
+    env = dict(os.environ, ARK_ORACLE_LIB=so, OMP_NUM_THREADS="2")
+    r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider",
+                        "-m", "not gpu"] + [os.path.join(ROOT, "tests", f"test_oracle_{f}.py")
+                                            for f in files],
+                       cwd=ROOT, env=env, capture_output=True, text=True, timeout=600)
+    return r.returncode, (r.stdout + r.stderr)[-1500:]
+
+
+@pytest.fixture(scope="module")
+def results(tmp_path_factory):
+    tmp = str(tmp_path_factory.mktemp("mutants"))
+    jobs = {"unmutated": (None, None, PINS)}
+    jobs.update(MUTANTS)
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        futs = {n: ex.submit(_build_and_run, tmp, n, *job) for n, job in jobs.items()}
+        return {n: f.result() for n, f in futs.items()}
+
+
+def test_unmutated_copy_passes_the_pins(results):
+    rc, out = results["unmutated"]
+    assert rc == 0, out
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_pins_catch_the_mutant(results, name):
+    rc, out = results[name]
+    assert rc == 1, f"{name}: pins {MUTANTS[name][2]} did not fail (exit {rc})\n{out}"
