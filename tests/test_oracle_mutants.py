@@ -1,13 +1,15 @@
 """The oracle's pins catch plausible mistakes.  Each mutant is a copy of
-oracle/ark_oracle.c with one planted error -- a swapped or dropped operand, a
-wrong sign, comparison, constant or index, a rounding shortcut -- compiled on
-the CPU with the oracle's own flags.  The pin tests named beside it must fail
-against that build.  Those pins are the independent checks: the second
+oracle/ark_oracle.c, or of the checkpoint format's oracle/ckpt.py, with one
+planted error -- a swapped or dropped operand, a wrong sign, comparison,
+constant or index, a rounding shortcut.  The C mutants are compiled on the
+CPU with the oracle's own flags.  The pin tests named beside each mutant must
+fail against it.  Those pins are the independent checks: the second
 restatement in Python with an exact-rational fma, closed forms, exhaustive
-conversions against F16C and numpy, brute force on small inputs, and the
-reference's own loss-scale trajectory.  Self-consistency checks (the
-vectorised loops against the scalar ones, fixtures the oracle wrote) are not
-run here.  An unmutated copy built the same way must pass them."""
+conversions against F16C and numpy, brute force on small inputs, the
+reference's own loss-scale trajectory, and a checkpoint file typed byte by
+byte from the format.  Self-consistency checks (the vectorised loops against
+the scalar ones, fixtures the oracle wrote) are not run here.  An unmutated
+copy built the same way must pass them."""
 import os
 import shutil
 import subprocess
@@ -73,6 +75,52 @@ MUTANTS = {
 }
 PINS = sorted({f for _, _, files in MUTANTS.values() for f in files})
 
+# The checkpoint format's restatement (oracle/ckpt.py, io.rs:432-671), pinned
+# by tests/test_oracle_ckpt.py (a known-answer file typed byte by byte from
+# the format, the loader's regrouping rules, V3/V2 layouts, failures).
+CKPT = os.path.join(ROOT, "oracle", "ckpt.py")
+CKPT_MUTANTS = {
+    "magic_in_reading_order": ("MAGIC_V4 = 0x4B345241", "MAGIC_V4 = 0x41524B34"),
+    "header_steps_swapped": ("MAGIC_V4, global_step, adam_step, n_tensors)]",
+                             "MAGIC_V4, adam_step, global_step, n_tensors)]"),
+    "f16_record_tagged_f32": ('return struct.pack("<QQ", d.size, 0)',
+                              'return struct.pack("<QQ", d.size, 1)'),
+    "gamma_final_moments_swapped": ("_rec_f32(gamma_f_m_f32), _rec_f32(gamma_f_v_f32)]",
+                                    "_rec_f32(gamma_f_v_f32), _rec_f32(gamma_f_m_f32)]"),
+    "unknown_type_read_as_f16": ("if version == 4 and tipo == 0:", "if version == 4 and tipo != 1:"),
+    "gamma_final_test": ("has_gamma_final = (n_tensors - 3) % 27 == 3",
+                         "has_gamma_final = (n_tensors - 3) % 27 == 0"),
+    "layer_m_slice": ("m += rem[base + 9:base + 18]", "m += rem[base + 8:base + 17]"),
+}
+
+_CKPT_DRIVER = """
+import importlib.util, sys
+sys.path.insert(0, {root!r})
+import oracle
+spec = importlib.util.spec_from_file_location("oracle.ckpt", {mutant!r})
+mod = importlib.util.module_from_spec(spec)
+sys.modules["oracle.ckpt"] = mod
+spec.loader.exec_module(mod)
+oracle.ckpt = mod
+import pytest
+sys.exit(pytest.main(["-q", "-x", "-p", "no:cacheprovider", "-m", "not gpu", {test!r}]))
+"""
+
+
+def _run_ckpt_mutant(tmp, name, old, new):
+    src = open(CKPT).read()
+    if old is not None:
+        assert src.count(old) == 1, f"{name}: the text to mutate is not in oracle/ckpt.py once"
+        src = src.replace(old, new)
+    path = os.path.join(tmp, f"ckpt_{name}.py")
+    with open(path, "w") as f:
+        f.write(src)
+    code = _CKPT_DRIVER.format(root=ROOT, mutant=path,
+                               test=os.path.join(ROOT, "tests", "test_oracle_ckpt.py"))
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True,
+                       timeout=600)
+    return r.returncode, (r.stdout + r.stderr)[-1500:]
+
 
 def _build_and_run(tmp, name, old, new, files):
     """Build ark_oracle.c with `old` replaced by `new` (None: unchanged) and
@@ -106,11 +154,16 @@ def results(tmp_path_factory):
     jobs.update(MUTANTS)
     with ThreadPoolExecutor(max_workers=4) as ex:
         futs = {n: ex.submit(_build_and_run, tmp, n, *job) for n, job in jobs.items()}
+        futs["ckpt:unmutated"] = ex.submit(_run_ckpt_mutant, tmp, "unmutated", None, None)
+        for n, (old, new) in CKPT_MUTANTS.items():
+            futs["ckpt:" + n] = ex.submit(_run_ckpt_mutant, tmp, n, old, new)
         return {n: f.result() for n, f in futs.items()}
 
 
 def test_unmutated_copy_passes_the_pins(results):
     rc, out = results["unmutated"]
+    assert rc == 0, out
+    rc, out = results["ckpt:unmutated"]
     assert rc == 0, out
 
 
@@ -118,3 +171,9 @@ def test_unmutated_copy_passes_the_pins(results):
 def test_pins_catch_the_mutant(results, name):
     rc, out = results[name]
     assert rc == 1, f"{name}: pins {MUTANTS[name][2]} did not fail (exit {rc})\n{out}"
+
+
+@pytest.mark.parametrize("name", sorted(CKPT_MUTANTS))
+def test_pins_catch_the_checkpoint_mutant(results, name):
+    rc, out = results["ckpt:" + name]
+    assert rc == 1, f"{name}: tests/test_oracle_ckpt.py did not fail (exit {rc})\n{out}"
