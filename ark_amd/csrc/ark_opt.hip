@@ -56,6 +56,7 @@ struct ark_opt_handle {
   uint32_t nseg = 0;
   int spb = 8;
   uint32_t norm_blocks = 0;
+  uint32_t nt_from = 0;  // norm blocks from here up stream past the cache
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
@@ -218,6 +219,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->nseg = (uint32_t)nseg;
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
+  h->nt_from = ark::sumsq_nt_from(spb, gsz);
 
   // One allocation: segments | block flags | partial sums | state | scalars | info
   size_t off = 0;
@@ -330,7 +332,7 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
   if (h->nseg) {
     ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
                               h->nseg, h->d_block_fast, h->d_state, h->d_part_sum,
-                              h->stream));
+                              h->nt_from, h->stream));
     if (h->d_fold)
       ARK_HIP(ark::launch_fold(h->padded_parts, h->d_part_sum, h->d_fold, h->stream));
   }
