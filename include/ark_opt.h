@@ -191,8 +191,9 @@ int ark_opt_get_timing(ark_opt_handle *h, ark_opt_timing *out);
 /* Drop-in for one call of ark_asm_adam_step_f16 (opti.s:189-193, declared
  * at optimizer.rs:20-23 and ffi.rs:105-108): same arguments in the same
  * order, fp32 gradients used as given (no unscale, no clip), t == 0 treated
- * as 1, plus the stream.  Runs the fused AdamW kernel on a one-tensor
- * table; returns once the work is queued. */
+ * as 1, plus the stream.  Runs the same per-row AdamW code as ark_opt_step
+ * over the one tensor, with the step scalars passed as kernel arguments
+ * (no table upload, nothing allocated); returns once the work is queued. */
 int ark_hip_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
                           uint64_t n, float lr, float beta1, float beta2,
                           float eps, float wd, uint32_t t, void *stream);
