@@ -238,3 +238,40 @@ def test_handoff_into_optimizer_step():
     assert c["w"] == 0 and c["m"] == 0 and c["v"] == 0, c
     opt.close()
     plan.close()
+
+
+def test_entry_points_reject_host_or_short_buffers():
+    """The accumulation, a gradient plan and the scatter check every buffer
+    on the host before any launch: host memory and a span longer than its
+    allocation are refused with EINVAL and a message naming the buffer."""
+    import ctypes as C
+    from ark_amd import _abi
+    from ark_amd._lib import lib
+    torch = _torch()
+    L = lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    dst = torch.zeros(1000, device="cuda")
+    src = torch.zeros(1000, device="cuda")
+    host = np.zeros(1000, np.float32)
+    assert L.ark_grad_accumulate(dst.data_ptr(), host.ctypes.data, 1000, None) == _abi.EINVAL
+    assert "host memory" in msg() or "not memory known" in msg(), msg()
+    assert L.ark_grad_accumulate(dst.data_ptr(), src.data_ptr(), 1 << 28, None) == _abi.EINVAL
+    assert "exceeds its allocation" in msg(), msg()
+    spans = (_abi.GradSpan * 2)()
+    spans[0] = _abi.GradSpan(dst.data_ptr(), src.data_ptr(), 1000)
+    spans[1] = _abi.GradSpan(dst.data_ptr(), host.ctypes.data, 1000)
+    h = C.c_void_p()
+    assert L.ark_grad_plan_create(spans, 2, None, C.byref(h)) == _abi.EINVAL
+    assert "buffer 1" in msg() and not h.value, msg()
+    g = torch.zeros(100, 64, device="cuda")
+    dx0 = torch.zeros(10, 64, device="cuda")
+    tokens = np.zeros(10, np.uint32)
+    rc = L.ark_grad_embed_scatter(g.data_ptr(), 100, 64, tokens.ctypes.data, dx0.data_ptr(), 10,
+                                  None)
+    assert rc == _abi.EINVAL and "tokens" in msg(), msg()
+    tok_dev = torch.zeros(1 << 22, dtype=torch.int32, device="cuda")  # 4M tokens, dx0 holds 10 rows
+    rc = L.ark_grad_embed_scatter(g.data_ptr(), 100, 64, tok_dev.data_ptr(), dx0.data_ptr(),
+                                  1 << 22, None)
+    assert rc == _abi.EINVAL and "dx0" in msg() and "exceeds its allocation" in msg(), msg()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(g).item() == 0 and torch.count_nonzero(dst).item() == 0
