@@ -328,3 +328,42 @@ def test_unpack_checks_headers():
     img[0] ^= 1
     with pytest.raises(ArkOptError, match="file header"):
         ckpt.unpack(img, y)
+
+
+def test_entry_points_reject_host_or_short_buffers(tmp_path):
+    """Save, pack and unpack check every record and the image on the host
+    before any launch or file: a record in host memory, a record past its
+    allocation and an image shorter than the layout are refused with EINVAL
+    and a message, and no file is created."""
+    import ctypes as C
+    import os
+    import torch
+    from ark_amd._lib import lib
+    L = lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    w = torch.zeros(1000, dtype=torch.float16, device="cuda")
+    m = torch.zeros(1000, device="cuda")
+    host = np.zeros(1000, np.float32)
+    recs = (_abi.CkptRecord * 2)()
+    recs[0] = _abi.CkptRecord(w.data_ptr(), 1000, _abi.CKPT_F16, 0)
+    recs[1] = _abi.CkptRecord(host.ctypes.data, 1000, _abi.CKPT_F32, 0)
+    path = str(tmp_path / "x.ark")
+    assert L.ark_ckpt_save_v4(os.fsencode(path), 1, 1, recs, 2, None, None) == _abi.EINVAL
+    assert "buffer 1" in msg() and not os.path.exists(path), msg()
+    image = torch.zeros(1 << 14, dtype=torch.uint8, device="cuda")
+    recs[1] = _abi.CkptRecord(m.data_ptr(), 1 << 28, _abi.CKPT_F32, 0)  # 1 GiB from m
+    rc = L.ark_ckpt_v4_pack(recs, 2, 1, 1, None, image.data_ptr(), image.numel(), None)
+    assert rc == _abi.EINVAL and "exceeds its allocation" in msg(), msg()
+    types = (C.c_uint32 * 2)(_abi.CKPT_F16, _abi.CKPT_F32)
+    rc = L.ark_ckpt_v4_unpack(image.data_ptr(), image.numel(), recs, 2, types, None)
+    assert rc == _abi.EINVAL and "exceeds its allocation" in msg(), msg()
+    recs[1] = _abi.CkptRecord(m.data_ptr(), 1000, _abi.CKPT_F32, 0)
+    need = C.c_uint64()
+    assert L.ark_ckpt_v4_image_bytes(recs, 2, 0, C.byref(need)) == 0
+    rc = L.ark_ckpt_v4_pack(recs, 2, 1, 1, None, image.data_ptr(), need.value - 1, None)
+    assert rc == _abi.EINVAL and "image holds" in msg(), msg()
+    # unpack reads the image size the caller states: 1 GiB is past the allocation
+    rc = L.ark_ckpt_v4_unpack(image.data_ptr(), 1 << 30, recs, 2, types, None)
+    assert rc == _abi.EINVAL and "image" in msg() and "exceeds its allocation" in msg(), msg()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(image).item() == 0
