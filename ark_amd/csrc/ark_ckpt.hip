@@ -860,9 +860,20 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
     }
   } eg{ev};
   StreamSync sync{s};
+  // Written to <path>.tmp and renamed over path once complete: a save that
+  // fails leaves no partial file (one that fallocate has sized in full would
+  // pass a loader's length checks) and any earlier checkpoint at path intact.
+  const std::string tmp = std::string(path) + ".tmp";
   Fd f;
-  f.fd = ::open(path, O_RDWR | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
-  if (f.fd < 0) return io_fail("create", path);
+  f.fd = ::open(tmp.c_str(), O_RDWR | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+  if (f.fd < 0) return io_fail("create", tmp.c_str());
+  struct TmpFile {
+    const std::string& name;
+    bool done = false;
+    ~TmpFile() {
+      if (!done) (void)::unlink(name.c_str());
+    }
+  } tmp_file{tmp};
   // Preferred: reserve the whole file, map it, and copy each chunk into the
   // mapping from several threads (writes to one file through write() are
   // serialised by the file's lock).  The reservation makes a full disk fail
@@ -894,15 +905,17 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
       ARK_HIP(hipEventSynchronize(ev[j & 1]));
       if (map.p)
         parallel_copy(map.p + off, pin[j & 1].p, len);
-      else if ((rc = parallel_io(true, f.fd, pin[j & 1].p, len, off, path)))
+      else if ((rc = parallel_io(true, f.fd, pin[j & 1].p, len, off, tmp.c_str())))
         return rc;
     }
   }
-  if (map.p && munmap(map.p, map.len) != 0) return io_fail("unmap", path);
+  if (map.p && munmap(map.p, map.len) != 0) return io_fail("unmap", tmp.c_str());
   map.p = nullptr;
   const int fd = f.fd;
   f.fd = -1;
-  if (::close(fd) != 0) return io_fail("close", path);
+  if (::close(fd) != 0) return io_fail("close", tmp.c_str());
+  if (::rename(tmp.c_str(), path) != 0) return io_fail("rename to", path);
+  tmp_file.done = true;
   return ARK_OPT_OK;
 }
 

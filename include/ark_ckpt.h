@@ -79,9 +79,11 @@ typedef struct ark_ckpt_info {
   uint32_t reserved;
 } ark_ckpt_info;
 
-/* CheckpointV3::save_fp16 (io.rs:432-500): writes path (created or
- * truncated).  amp may be NULL (no trailer).  The records are read on the
- * given stream; the call returns when the file is written and closed. */
+/* CheckpointV3::save_fp16 (io.rs:432-500): writes the file as
+ * "<path>.tmp" and renames it to path once complete, so a failed save
+ * leaves no partial file and an existing file at path unchanged.  amp may be
+ * NULL (no trailer).  The records are read on the given stream; the call
+ * returns when the file is written, closed and renamed. */
 int ark_ckpt_save_v4(const char *path, uint64_t global_step, uint64_t adam_step,
                      const ark_ckpt_record *records, int32_t n_records,
                      const ark_opt_state *amp, void *stream);

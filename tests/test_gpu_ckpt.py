@@ -367,3 +367,19 @@ def test_entry_points_reject_host_or_short_buffers(tmp_path):
     assert rc == _abi.EINVAL and "image" in msg() and "exceeds its allocation" in msg(), msg()
     torch.cuda.synchronize()
     assert torch.count_nonzero(image).item() == 0
+
+
+def test_save_replaces_the_file_whole(tmp_path):
+    """A save goes through <path>.tmp and a rename: afterwards only the
+    finished file is there, and it replaces an earlier one completely."""
+    import os
+    import torch
+    path = tmp_path / "ckpt.ark"
+    path.write_bytes(b"an earlier, longer file " * 1000)
+    w = torch.arange(777, dtype=torch.float32, device="cuda").half()
+    m = torch.full((777,), 0.5, device="cuda")
+    ckpt.save(str(path), [w, m], 12, 34)
+    torch.cuda.synchronize()
+    assert sorted(os.listdir(tmp_path)) == ["ckpt.ark"]
+    want = K.write_v4(12, 34, [w.cpu().numpy().view(np.uint16), m.cpu().numpy()])
+    assert path.read_bytes() == want
