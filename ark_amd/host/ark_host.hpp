@@ -99,7 +99,10 @@ inline float lr_now(const AdamConfig& cfg, uint32_t step) {
   const float decay_steps = (float)(step - cfg.warmup_steps);
   const float total_decay = 800000.0f;
   const float progress = fminf(decay_steps / total_decay, 1.0f);
-  const float cosine = 0.5f * (1.0f + cosf(3.14159274101257324f * progress));
+  // f32::cos as the correctly rounded fp32 cosine: libm's double cos rounded
+  // once, which is exact rounding over every argument this schedule makes.
+  const float cosine =
+      0.5f * (1.0f + (float)::cos((double)(3.14159274101257324f * progress)));
   const float lr_min = cfg.lr * 0.1f;
   return lr_min + (cfg.lr - lr_min) * cosine;
 }

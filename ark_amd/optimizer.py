@@ -14,6 +14,7 @@ Device memory and streams come from torch; every optimizer computation runs
 in the HIP library through its C ABI.
 """
 import ctypes as C
+import math
 from dataclasses import dataclass
 
 import numpy as np
@@ -58,6 +59,15 @@ def hparams(cfg: AdamConfig, amp: AmpConfig, grad_dtype=_abi.GRAD_F16):
     return hp
 
 
+def cos_f32(x) -> np.float32:
+    """The fp32 cosine of `f32::cos` (optimizer.rs:89), taken as the
+    correctly rounded result: libm's double cos, rounded once to fp32.  Over
+    every argument lr_now can pass (pi * d / 800000 in fp32, d = 0..800000)
+    this equals the exactly rounded cosine; the C++ mirror computes it the
+    same way."""
+    return np.float32(math.cos(float(np.float32(x))))
+
+
 def lr_now(cfg: AdamConfig, step: int) -> float:
     """optimizer.rs:80-92 in fp32, with `step` the already-incremented
     Optimizer::step (step_all increments before calling it, :172-173)."""
@@ -67,7 +77,7 @@ def lr_now(cfg: AdamConfig, step: int) -> float:
         return float(lr * (f32(step) + f32(1.0)) / f32(cfg.warmup_steps))
     decay_steps = f32(step - cfg.warmup_steps)
     progress = min(decay_steps / f32(800_000.0), f32(1.0))
-    cosine = f32(0.5) * (f32(1.0) + np.cos(f32(np.pi) * progress, dtype=np.float32))
+    cosine = f32(0.5) * (f32(1.0) + cos_f32(f32(np.pi) * progress))
     lr_min = lr * f32(0.1)
     return float(lr_min + (lr - lr_min) * cosine)
 
