@@ -12,7 +12,7 @@ settles it.  The two mirrors then agree bit for bit on every step."""
 import math
 import os
 import subprocess
-from decimal import Decimal, getcontext
+from decimal import Decimal, localcontext
 from fractions import Fraction
 
 import numpy as np
@@ -37,16 +37,17 @@ def schedule_args():
 
 def dec_cos(x: float) -> Decimal:
     """cos(x) to ~60 significant digits by its Taylor series (|x| <= 3.15)."""
-    getcontext().prec = 70
-    x = Decimal(x)
-    x2 = x * x
-    term, total, k = Decimal(1), Decimal(1), 0
-    while True:
-        k += 1
-        term = -term * x2 / ((2 * k - 1) * (2 * k))
-        total += term
-        if abs(term) < Decimal("1e-66"):
-            return total
+    with localcontext() as ctx:
+        ctx.prec = 70
+        x = Decimal(x)
+        x2 = x * x
+        term, total, k = Decimal(1), Decimal(1), 0
+        while True:
+            k += 1
+            term = -term * x2 / ((2 * k - 1) * (2 * k))
+            total += term
+            if abs(term) < Decimal("1e-66"):
+                return total
 
 
 def round_exact_to_f32(v: Decimal) -> np.float32:
@@ -92,10 +93,12 @@ def test_cos_f32_known_answers():
     """Closed forms independent of libm: fp32(pi) = pi + delta, so
     cos(fp32(pi) / 2) = -sin(delta / 2) = -delta / 2 to fp32 precision, and
     cos(fp32(pi)) = -cos(delta) rounds to -1."""
-    getcontext().prec = 70
-    delta = Decimal(float(F32(np.pi))) - Decimal(PI_DIGITS)
+    with localcontext() as ctx:
+        ctx.prec = 70
+        delta = Decimal(float(F32(np.pi))) - Decimal(PI_DIGITS)
+        minus_half_delta = -delta / 2
     half = F32(F32(np.pi) * F32(0.5))
-    assert cos_f32(half) == round_exact_to_f32(-delta / 2)
+    assert cos_f32(half) == round_exact_to_f32(minus_half_delta)
     assert cos_f32(F32(np.pi)) == F32(-1.0)
     assert cos_f32(F32(0.0)) == F32(1.0)
 
@@ -131,11 +134,19 @@ def test_python_mirror_follows_the_schedule(lr, warmup):
     assert lr_now(cfg, 10 * TOTAL_DECAY) == float(F32(lr) * F32(0.1))
 
 
+@pytest.fixture(scope="module")
+def lr_table():
+    """The C++ mirror's table tool, built with hipcc when absent (host code only)."""
+    if not os.path.exists(LR_TABLE):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp"), "_build/lr_table"],
+                       check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    return LR_TABLE
+
+
 @pytest.mark.parametrize("lr,warmup", [(3e-4, 100), (1e-3, 2000)])
-def test_cpp_mirror_equals_python_mirror_on_every_step(lr, warmup):
-    assert os.path.exists(LR_TABLE), f"{LR_TABLE} is not built: run __graft_entry__.build()"
+def test_cpp_mirror_equals_python_mirror_on_every_step(lr_table, lr, warmup):
     n = warmup + TOTAL_DECAY + 10
-    r = subprocess.run([LR_TABLE, repr(lr), str(warmup), str(n)], stdout=subprocess.PIPE,
+    r = subprocess.run([lr_table, repr(lr), str(warmup), str(n)], stdout=subprocess.PIPE,
                        timeout=120, check=True)
     cpp = np.frombuffer(r.stdout, dtype=np.float32)
     assert len(cpp) == n
