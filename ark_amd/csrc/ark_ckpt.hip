@@ -579,6 +579,19 @@ int io_fail(const char* what, const char* path) {
   return fail(ARK_OPT_EIO, "%s %s: %s", what, path, strerror(errno));
 }
 
+// Flushes the directory holding path so a rename into it is durable.  Best
+// effort: some file systems refuse fsync on a directory, and the file itself
+// is complete either way.
+void sync_parent_dir(const char* path) {
+  std::string dir(path);
+  const size_t slash = dir.find_last_of('/');
+  dir = slash == std::string::npos ? std::string(".") : dir.substr(0, slash ? slash : 1);
+  const int d = ::open(dir.c_str(), O_RDONLY | O_DIRECTORY | O_CLOEXEC);
+  if (d < 0) return;
+  (void)fsync(d);
+  (void)::close(d);
+}
+
 int read_exact(int fd, void* buf, uint64_t len, uint64_t off, const char* path) {
   uint8_t* p = (uint8_t*)buf;
   while (len) {
@@ -911,11 +924,15 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
   }
   if (map.p && munmap(map.p, map.len) != 0) return io_fail("unmap", tmp.c_str());
   map.p = nullptr;
+  // The data reaches the disk before the rename does, so a crash of the
+  // machine cannot leave path naming a file whose pages were never written.
+  if (fdatasync(f.fd) != 0) return io_fail("flush", tmp.c_str());
   const int fd = f.fd;
   f.fd = -1;
   if (::close(fd) != 0) return io_fail("close", tmp.c_str());
   if (::rename(tmp.c_str(), path) != 0) return io_fail("rename to", path);
   tmp_file.done = true;
+  sync_parent_dir(path);
   return ARK_OPT_OK;
 }
 
