@@ -364,6 +364,7 @@ int ark_opt_record_overflow(ark_opt_handle* h, ark_opt_step_info* info) {
 int ark_opt_get_state(ark_opt_handle* h, ark_opt_state* out) {
   if (!h || !out) return fail(ARK_OPT_EINVAL, "handle or out is NULL");
   DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   ARK_HIP(hipMemcpyAsync(h->h_state, h->d_state, sizeof(ark_opt_state),
                          hipMemcpyDeviceToHost, h->stream));
   ARK_HIP(hipStreamSynchronize(h->stream));
@@ -376,6 +377,7 @@ int ark_opt_set_state(ark_opt_handle* h, const ark_opt_state* st) {
   if (!finite_f(st->loss_scale) || !(st->loss_scale > 0.0f))
     return fail(ARK_OPT_EINVAL, "loss_scale must be finite and > 0");
   DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   ARK_HIP(hipStreamSynchronize(h->stream));
   *h->h_state = *st;
   ARK_HIP(hipMemcpyAsync(h->d_state, h->h_state, sizeof(ark_opt_state),
@@ -387,6 +389,7 @@ int ark_opt_set_state(ark_opt_handle* h, const ark_opt_state* st) {
 int ark_opt_set_timing(ark_opt_handle* h, int enable) {
   if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
   DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   if (enable && h->ev.empty()) {
     h->ev.resize(4 * kTimingPool);
     for (auto& e : h->ev) ARK_HIP(hipEventCreate(&e));
@@ -402,6 +405,7 @@ int ark_opt_set_timing(ark_opt_handle* h, int enable) {
 int ark_opt_get_timing(ark_opt_handle* h, ark_opt_timing* out) {
   if (!h || !out) return fail(ARK_OPT_EINVAL, "handle or out is NULL");
   DeviceGuard g(h->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   int rc = fold_timing(h);
   if (rc) return rc;
   *out = h->acc;
