@@ -12,12 +12,12 @@
 //       arbitrary order and change the fp32 sums, so instead:
 //         1. key = clamped token, value = position i, and a stable LSD radix
 //            sort of (key, i) over the key's bits, which keeps equal keys in
-//            increasing i: for up to kBlockSortMax tokens (the reference's
+//            increasing i: for up to kSortTile tokens (the reference's
 //            2 x 2048 batch) one block sorts them in LDS (block_sort_kernel),
-//            beyond that keys_kernel and hipCUB's device radix sort;
-//         3. gather_kernel: the dx0 rows copied in sorted order into a
+//            beyond that one hist/scan/scatter launch triple per 8-bit digit;
+//         2. gather_kernel: the dx0 rows copied in sorted order into a
 //            workspace, so every run of equal keys is contiguous;
-//         4. run_kernel: one 256-lane block per (run of equal keys,
+//         3. run_kernel: one 256-lane block per (run of equal keys,
 //            256-column tile) finds the run's end by binary search, loads the
 //            embedding row once, adds the run's rows in sorted (= original)
 //            order and stores it once.  A run of kLongRun rows or more gives
@@ -29,7 +29,6 @@
 //       the CPU loop, and the result is bit-identical.
 #include <string.h>
 
-#include <hipcub/hipcub.hpp>
 #include <vector>
 
 #include "ark_common.hpp"
@@ -107,55 +106,266 @@ __global__ __launch_bounds__(kWave) void grad_batch(const GradSeg* __restrict__ 
   }
 }
 
-// Up to kBlockSortMax tokens: one block loads them (key = clamped token,
-// value = position, bridge.m:923), sorts the pairs over bits [0, end_bit)
-// with the stable block radix sort, and writes them out.  Input and output
-// are in blocked order (thread t holds positions t*kSortItems..), so the
-// stable sort keeps equal keys in increasing position.  Padding past n takes
-// the all-ones key: it ties with the largest real key at most and, coming
-// later in the input, sorts after it.
+// ---- stable LSD radix sort of (clamped token, position) ------------------
+// A block of kSortThreads threads holds a tile of kSortTile items: item j of
+// lane l of wave w sits at tile position w*256 + j*64 + l, so the order
+// (wave, item, lane) is the position order.  One pass sorts the tile by
+// kRadixBits bits of the key:
+//   rank   per item, how many items of its wave with the same digit precede
+//          it, from ballots of the digit's bits (wave_rank); the digit's
+//          last item in the wave also writes the wave's count of it into an
+//          LDS table laid out digit-major, (digit, wave);
+//   scan   an exclusive block scan of that table gives every (digit, wave)
+//          the number of tile items before it in (digit, position) order;
+//   place  item -> scan[digit, wave] + rank.
+// Equal digits keep their position order, so each pass is stable and the
+// passes from the low bits up (LSD) leave the keys sorted with equal keys in
+// increasing position: the order in which bridge.m:922-928's loop visits a
+// token's rows.  Up to one tile (the reference's 2 x 2048 batch) one block
+// does every pass in LDS (block_sort_kernel); past that each pass is three
+// launches: per-tile digit counts (sort_hist_kernel), their exclusive scan
+// in (digit, tile) order (sort_scan_kernel), and the tile-local rank plus the
+// scanned count as the global destination (sort_scatter_kernel).
 constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / kWave;                // 16
 constexpr int kSortItems = 4;
-constexpr uint32_t kBlockSortMax = kSortThreads * kSortItems;  // 4096
+constexpr uint32_t kSortTile = kSortThreads * kSortItems;       // 4096
+constexpr int kRadixBits = 8;
+constexpr uint32_t kRadix = 1u << kRadixBits;                   // 256
+constexpr uint32_t kHist = kRadix * kSortWaves;                 // 4096
+constexpr uint32_t kPadKey = 0xFFFFFFFFu;
+static_assert(kHist == kSortThreads * 4, "block_exclusive takes 4 entries per thread");
+static_assert(kSortWaves * kSortItems * kWave == (int)kSortTile, "tile layout");
 
+// bridge.m:923: t = tokens[i] < vocab ? tokens[i] : 0
+__device__ __forceinline__ uint32_t clamp_token(uint32_t t, uint32_t vocab) {
+  return t < vocab ? t : 0u;
+}
+
+__device__ __forceinline__ uint32_t tile_pos(uint32_t wave, int j, uint32_t lane) {
+  return wave * (kSortItems * kWave) + (uint32_t)j * kWave + lane;
+}
+
+// rank[j] = the number of items of this wave with digit dig[j] that precede
+// item j in (item, lane) order.  The last such item of each digit writes the
+// wave's count of the digit to hist[digit * kSortWaves + wave]; entries of
+// digits absent from the wave are left as they are (zero).
+__device__ __forceinline__ void wave_rank(const uint32_t (&dig)[kSortItems],
+                                          uint32_t (&rank)[kSortItems], uint32_t* hist,
+                                          uint32_t wave) {
+  const uint32_t lane = __lane_id();
+  const uint64_t below = (1ull << lane) - 1ull;
+  const uint64_t above = ~((2ull << lane) - 1ull);  // lane 63: 2 << 63 wraps to 0
+  uint64_t bal[kSortItems][kRadixBits];
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i)
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) bal[i][b] = __ballot((dig[i] >> b) & 1u);
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    uint64_t same[kSortItems];  // lanes whose item i has digit dig[j]
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+      uint64_t m = ~0ull;
+#pragma unroll
+      for (int b = 0; b < kRadixBits; ++b) m &= ((dig[j] >> b) & 1u) ? bal[i][b] : ~bal[i][b];
+      same[i] = m;
+    }
+    uint32_t r = (uint32_t)__popcll(same[j] & below);
+    bool last = (same[j] & above) == 0ull;
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+      if (i < j) r += (uint32_t)__popcll(same[i]);
+      if (i > j) last = last && same[i] == 0ull;
+    }
+    rank[j] = r;
+    if (last) hist[dig[j] * kSortWaves + wave] = r + 1u;
+  }
+}
+
+// Exclusive prefix over the block's kSortThreads x 4 values in thread order
+// (thread t holds entries 4t .. 4t+3): e[i] becomes carry plus every entry
+// before it; returns carry plus all entries.  Every thread of the block
+// calls it; wsum is LDS scratch of kSortWaves words.
+__device__ __forceinline__ uint32_t block_exclusive(uint32_t (&e)[4], uint32_t* wsum,
+                                                    uint32_t carry) {
+  const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+  const uint32_t s = e[0] + e[1] + e[2] + e[3];
+  uint32_t incl = s;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o, kWave);
+    if (lane >= (uint32_t)o) incl += y;
+  }
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = carry, total = carry;
+#pragma unroll
+  for (int w = 0; w < kSortWaves; ++w) {
+    const uint32_t x = wsum[w];
+    if ((uint32_t)w < wave) before += x;
+    total += x;
+  }
+  uint32_t run = before + incl - s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t x = e[i];
+    e[i] = run;
+    run += x;
+  }
+  __syncthreads();  // wsum is free for the next call
+  return total;
+}
+
+// One pass of the tile in registers: zero the (digit, wave) table, rank,
+// scan.  On return hist[d * kSortWaves + w] holds the number of tile items
+// (padding included) before (digit d, wave w) in (digit, position) order.
+__device__ __forceinline__ void tile_pass(const uint32_t (&dig)[kSortItems],
+                                          uint32_t (&rank)[kSortItems], uint32_t* hist,
+                                          uint32_t* wsum) {
+  const uint32_t t = threadIdx.x, wave = t / kWave;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hist[4 * t + i] = 0u;
+  __syncthreads();
+  wave_rank(dig, rank, hist, wave);
+  __syncthreads();
+  uint32_t e[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = hist[4 * t + i];
+  block_exclusive(e, wsum, 0u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hist[4 * t + i] = e[i];
+  __syncthreads();
+}
+
+// Up to kSortTile tokens: one block sorts (key = clamped token, value =
+// position) over bits [0, end_bit) in LDS and writes the first n pairs.
+// Positions past n take the all-ones key: its digit is the largest in every
+// pass and it comes after every real item, so it sorts after them all.
 __global__ __launch_bounds__(kSortThreads) void block_sort_kernel(
     const uint32_t* __restrict__ tokens, uint32_t n, uint32_t vocab, int end_bit,
     uint32_t* __restrict__ skeys, uint32_t* __restrict__ svals) {
-  typedef hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortItems, uint32_t> Sort;
-  __shared__ typename Sort::TempStorage tmp;
-  uint32_t k[kSortItems], v[kSortItems];
+  __shared__ uint32_t s_keys[kSortTile], s_vals[kSortTile], s_hist[kHist], s_wsum[kSortWaves];
+  const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+  uint32_t k[kSortItems], v[kSortItems], dg[kSortItems], r[kSortItems];
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
-    const uint32_t i = threadIdx.x * kSortItems + j;
-    uint32_t t = 0xFFFFFFFFu;
-    if (i < n) {
-      t = ld_g<uint32_t>(tokens + i);
-      t = t < vocab ? t : 0u;
-    }
-    k[j] = t;
-    v[j] = i;
+    const uint32_t p = tile_pos(wave, j, lane);
+    k[j] = p < n ? clamp_token(ld_g<uint32_t>(tokens + p), vocab) : kPadKey;
+    v[j] = p;
   }
-  Sort(tmp).Sort(k, v, 0, end_bit);
+  for (int shift = 0; shift < end_bit; shift += kRadixBits) {
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) dg[j] = (k[j] >> shift) & (kRadix - 1u);
+    tile_pass(dg, r, s_hist, s_wsum);
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+      const uint32_t dst = s_hist[dg[j] * kSortWaves + wave] + r[j];
+      s_keys[dst] = k[j];
+      s_vals[dst] = v[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+      const uint32_t p = tile_pos(wave, j, lane);
+      k[j] = s_keys[p];
+      v[j] = s_vals[p];
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
-    const uint32_t i = threadIdx.x * kSortItems + j;
-    if (i < n) {
-      skeys[i] = k[j];
-      svals[i] = v[j];
+    const uint32_t p = tile_pos(wave, j, lane);
+    if (p < n) {
+      skeys[p] = k[j];
+      svals[p] = v[j];
     }
   }
 }
 
-// bridge.m:923: t = tokens[i] < vocab ? tokens[i] : 0
-__global__ __launch_bounds__(kThreads) void keys_kernel(const uint32_t* __restrict__ tokens,
-                                                        uint32_t n, uint32_t vocab,
-                                                        uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ vals) {
-  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t t = ld_g<uint32_t>(tokens + i);
-  keys[i] = t < vocab ? t : 0u;
-  vals[i] = i;
+// counts[d * tiles + tile] = the items of the tile whose key has digit d at
+// this pass.  from_tokens: the keys are the clamped tokens (first pass).
+__global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(
+    const uint32_t* __restrict__ keys, uint32_t from_tokens, uint32_t n, uint32_t vocab,
+    int shift, uint32_t* __restrict__ counts, uint32_t tiles) {
+  __shared__ uint32_t h[kRadix];
+  if (threadIdx.x < kRadix) h[threadIdx.x] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t p = blockIdx.x * kSortTile + (uint32_t)j * kSortThreads + threadIdx.x;
+    if (p < n) {
+      uint32_t key = ld_g<uint32_t>(keys + p);
+      if (from_tokens) key = clamp_token(key, vocab);
+      atomicAdd(&h[(key >> shift) & (kRadix - 1u)], 1u);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kRadix) counts[threadIdx.x * tiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// counts[0, total) <- its exclusive prefix sums: one block, kSortTile
+// entries per round with the running total carried.
+__global__ __launch_bounds__(kSortThreads) void sort_scan_kernel(uint32_t* __restrict__ counts,
+                                                                 uint32_t total) {
+  __shared__ uint32_t wsum[kSortWaves];
+  uint32_t carry = 0;
+  for (uint32_t base = 0; base < total; base += kSortTile) {
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = base + 4u * threadIdx.x + (uint32_t)i;
+      e[i] = q < total ? counts[q] : 0u;
+    }
+    carry = block_exclusive(e, wsum, carry);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = base + 4u * threadIdx.x + (uint32_t)i;
+      if (q < total) counts[q] = e[i];
+    }
+  }
+}
+
+// One pass over a tile: item -> counts[digit * tiles + tile] (the items of
+// smaller digits, and of this digit in earlier tiles) + its rank among the
+// tile's items of the same digit.  The last tile's positions past n carry
+// the all-ones key (largest digit, last in position order), so they rank
+// after every real item and are not written.
+__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+    uint32_t from_tokens, uint32_t n, uint32_t vocab, int shift,
+    const uint32_t* __restrict__ counts, uint32_t tiles, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out) {
+  __shared__ uint32_t s_hist[kHist], s_wsum[kSortWaves];
+  const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave, tile = blockIdx.x;
+  uint32_t k[kSortItems], v[kSortItems], dg[kSortItems], r[kSortItems];
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t p = tile * kSortTile + tile_pos(wave, j, lane);
+    k[j] = kPadKey;
+    v[j] = 0u;
+    if (p < n) {
+      k[j] = ld_g<uint32_t>(keys_in + p);
+      if (from_tokens) {
+        k[j] = clamp_token(k[j], vocab);
+        v[j] = p;
+      } else {
+        v[j] = ld_g<uint32_t>(vals_in + p);
+      }
+    }
+    dg[j] = (k[j] >> shift) & (kRadix - 1u);
+  }
+  tile_pass(dg, r, s_hist, s_wsum);
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t p = tile * kSortTile + tile_pos(wave, j, lane);
+    if (p < n) {
+      const uint32_t d = dg[j];
+      const uint32_t dst = counts[d * tiles + tile] +
+                           (s_hist[d * kSortWaves + wave] - s_hist[d * kSortWaves]) + r[j];
+      keys_out[dst] = k[j];
+      vals_out[dst] = v[j];
+    }
+  }
 }
 
 // Row q of xs = row svals[q] of dx0 (d floats each); one block per row.
@@ -256,6 +466,105 @@ constexpr uint64_t kMaxFlatBlocks = 1u << 20;
 using ark::overlaps;
 
 using ark::StreamBuf;
+
+// Byte offsets of the scatter's workspace arrays, each 256-byte aligned:
+// the sorted keys and positions, for more than one tile a second pair that
+// the sort passes alternate with and the (digit, tile) counts, then the
+// copy of dx0 in sorted order.
+struct ScatterLayout {
+  uint32_t tiles = 0;  // kSortTile-item tiles; 1 = the one-block sort
+  size_t skeys = 0, svals = 0, keys = 0, vals = 0, counts = 0, xs = 0, bytes = 0;
+};
+
+ScatterLayout scatter_layout(uint32_t n, uint32_t d) {
+  ScatterLayout L;
+  L.tiles = (n + kSortTile - 1) / kSortTile;
+  const size_t arr = ark::align_up((size_t)n * 4, 256);
+  size_t off = 0;
+  L.skeys = off, off += arr;
+  L.svals = off, off += arr;
+  if (L.tiles > 1) {
+    L.keys = off, off += arr;
+    L.vals = off, off += arr;
+    L.counts = off, off += ark::align_up((size_t)kRadix * L.tiles * 4, 256);
+  }
+  L.xs = off, off += ark::align_up((size_t)n * d * 4, 256);
+  L.bytes = off;
+  return L;
+}
+
+// Argument checks shared by the scatter's entry points; *skip is set when
+// there is nothing to do.
+int scatter_check(const float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t* tokens,
+                  const float* dx0, uint32_t batch_seq, bool* skip) {
+  *skip = batch_seq == 0 || d == 0;
+  if (*skip) return ARK_OPT_OK;
+  if (vocab == 0) return fail(ARK_OPT_EINVAL, "vocab is 0");
+  if (batch_seq > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "batch_seq too large");
+  if (((uint64_t)d + kTileCols - 1) / kTileCols > 65535u) return fail(ARK_OPT_EINVAL, "d too large");
+  if (((uintptr_t)embed_grad & 3u) || ((uintptr_t)dx0 & 3u) || ((uintptr_t)tokens & 3u))
+    return fail(ARK_OPT_EINVAL, "embed_grad, dx0 or tokens not 4-byte aligned");
+  const uint64_t gbytes = (uint64_t)vocab * d * 4, xbytes = (uint64_t)batch_seq * d * 4;
+  int rc;
+  if ((rc = ark::check_buffer(embed_grad, gbytes, "embed_grad", 0))) return rc;
+  if ((rc = ark::check_buffer(dx0, xbytes, "dx0", 0))) return rc;
+  if ((rc = ark::check_buffer(tokens, (uint64_t)batch_seq * 4, "tokens", 0))) return rc;
+  if (overlaps(embed_grad, gbytes, dx0, xbytes))
+    return fail(ARK_OPT_EINVAL, "embed_grad and dx0 overlap");
+  return ARK_OPT_OK;
+}
+
+// Queues the scatter on s with its workspace at ws (L.bytes bytes, 256-byte
+// aligned): the sort, the row copy and the run adds.
+int scatter_launch(float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t* tokens,
+                   const float* dx0, uint32_t n, char* ws, const ScatterLayout& L,
+                   hipStream_t s) {
+  int end_bit = 1;
+  while (end_bit < 32 && ((vocab - 1u) >> end_bit) != 0u) ++end_bit;
+  uint32_t* skeys = (uint32_t*)(ws + L.skeys);
+  uint32_t* svals = (uint32_t*)(ws + L.svals);
+  float* xs = (float*)(ws + L.xs);
+  if (L.tiles == 1) {
+    hipLaunchKernelGGL(block_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, tokens, n, vocab,
+                       end_bit, skeys, svals);
+    ARK_HIP(hipGetLastError());
+  } else {
+    uint32_t* keys = (uint32_t*)(ws + L.keys);
+    uint32_t* vals = (uint32_t*)(ws + L.vals);
+    uint32_t* counts = (uint32_t*)(ws + L.counts);
+    const int passes = (end_bit + kRadixBits - 1) / kRadixBits;
+    const uint32_t* in_k = tokens;
+    const uint32_t* in_v = nullptr;
+    for (int pass = 0; pass < passes; ++pass) {
+      const int shift = pass * kRadixBits;
+      const uint32_t from_tokens = pass == 0 ? 1u : 0u;
+      // the last pass writes skeys/svals; the ones before alternate back
+      const bool to_sorted = ((passes - 1 - pass) & 1) == 0;
+      uint32_t* out_k = to_sorted ? skeys : keys;
+      uint32_t* out_v = to_sorted ? svals : vals;
+      hipLaunchKernelGGL(sort_hist_kernel, dim3(L.tiles), dim3(kSortThreads), 0, s, in_k,
+                         from_tokens, n, vocab, shift, counts, L.tiles);
+      ARK_HIP(hipGetLastError());
+      hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kSortThreads), 0, s, counts,
+                         kRadix * L.tiles);
+      ARK_HIP(hipGetLastError());
+      hipLaunchKernelGGL(sort_scatter_kernel, dim3(L.tiles), dim3(kSortThreads), 0, s, in_k, in_v,
+                         from_tokens, n, vocab, shift, (const uint32_t*)counts, L.tiles, out_k,
+                         out_v);
+      ARK_HIP(hipGetLastError());
+      in_k = out_k;
+      in_v = out_v;
+    }
+  }
+  const uint32_t gvec = ((d % 4u) == 0 && (((uintptr_t)dx0 & 15u) == 0)) ? 1u : 0u;
+  hipLaunchKernelGGL(gather_kernel, dim3(n), dim3(kThreads), 0, s, dx0, svals, d, gvec, xs);
+  ARK_HIP(hipGetLastError());
+  const uint32_t vec = ((d % 4u) == 0 && (((uintptr_t)embed_grad & 15u) == 0)) ? 1u : 0u;
+  const dim3 grid(n, (d + kTileCols - 1) / kTileCols);
+  hipLaunchKernelGGL(run_kernel, grid, dim3(kTileCols), 0, s, embed_grad, d, xs, skeys, n, vec);
+  ARK_HIP(hipGetLastError());
+  return ARK_OPT_OK;
+}
 
 }  // namespace
 
@@ -360,65 +669,18 @@ int ark_grad_plan_destroy(ark_grad_plan* p) {
 
 int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t* tokens,
                            const float* dx0, uint32_t batch_seq, void* stream) {
-  if (batch_seq == 0 || d == 0) return ARK_OPT_OK;
-  if (vocab == 0) return fail(ARK_OPT_EINVAL, "vocab is 0");
-  if (batch_seq > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "batch_seq too large");
-  if (((uint64_t)d + kTileCols - 1) / kTileCols > 65535u) return fail(ARK_OPT_EINVAL, "d too large");
-  if (((uintptr_t)embed_grad & 3u) || ((uintptr_t)dx0 & 3u) || ((uintptr_t)tokens & 3u))
-    return fail(ARK_OPT_EINVAL, "embed_grad, dx0 or tokens not 4-byte aligned");
-  const uint64_t gbytes = (uint64_t)vocab * d * 4, xbytes = (uint64_t)batch_seq * d * 4;
-  int rc;
-  if ((rc = ark::check_buffer(embed_grad, gbytes, "embed_grad", 0))) return rc;
-  if ((rc = ark::check_buffer(dx0, xbytes, "dx0", 0))) return rc;
-  if ((rc = ark::check_buffer(tokens, (uint64_t)batch_seq * 4, "tokens", 0))) return rc;
-  if (overlaps(embed_grad, gbytes, dx0, xbytes))
-    return fail(ARK_OPT_EINVAL, "embed_grad and dx0 overlap");
+  bool skip = false;
+  int rc = scatter_check(embed_grad, vocab, d, tokens, dx0, batch_seq, &skip);
+  if (rc || skip) return rc;
   hipStream_t s = (hipStream_t)stream;
-  int end_bit = 1;
-  while (end_bit < 32 && ((vocab - 1u) >> end_bit) != 0u) ++end_bit;
-  const int n = (int)batch_seq;
-  const bool block_sort = batch_seq <= kBlockSortMax;
-  size_t temp = 0;
-  if (!block_sort)
-    ARK_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (const uint32_t*)nullptr,
-                                               (uint32_t*)nullptr, (const uint32_t*)nullptr,
-                                               (uint32_t*)nullptr, n, 0, end_bit, s));
-  const size_t arr = ark::align_up((size_t)batch_seq * 4, 256);
-  const size_t rows = ark::align_up((size_t)xbytes, 256);
-  const size_t ws_bytes = 4 * arr + rows + temp;
+  const ScatterLayout L = scatter_layout(batch_seq, d);
   StreamBuf ws;
-  hipError_t e = ws.alloc(ws_bytes, s);
+  hipError_t e = ws.alloc(L.bytes, s);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", ws_bytes);
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", L.bytes);
   }
-  uint32_t* keys = (uint32_t*)ws.p;
-  uint32_t* vals = (uint32_t*)((char*)ws.p + arr);
-  uint32_t* skeys = (uint32_t*)((char*)ws.p + 2 * arr);
-  uint32_t* svals = (uint32_t*)((char*)ws.p + 3 * arr);
-  float* xs = (float*)((char*)ws.p + 4 * arr);
-  void* tmp = (char*)ws.p + 4 * arr + rows;
-  if (block_sort) {
-    hipLaunchKernelGGL(block_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, tokens, batch_seq,
-                       vocab, end_bit, skeys, svals);
-    ARK_HIP(hipGetLastError());
-  } else {
-    hipLaunchKernelGGL(keys_kernel, dim3((batch_seq + kThreads - 1) / kThreads), dim3(kThreads),
-                       0, s, tokens, batch_seq, vocab, keys, vals);
-    ARK_HIP(hipGetLastError());
-    ARK_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, temp, keys, skeys, vals, svals, n, 0,
-                                               end_bit, s));
-  }
-  const uint32_t gvec = ((d % 4u) == 0 && (((uintptr_t)dx0 & 15u) == 0)) ? 1u : 0u;
-  hipLaunchKernelGGL(gather_kernel, dim3(batch_seq), dim3(kThreads), 0, s, dx0, svals, d, gvec,
-                     xs);
-  ARK_HIP(hipGetLastError());
-  const uint32_t vec = ((d % 4u) == 0 && (((uintptr_t)embed_grad & 15u) == 0)) ? 1u : 0u;
-  const dim3 grid(batch_seq, (d + kTileCols - 1) / kTileCols);
-  hipLaunchKernelGGL(run_kernel, grid, dim3(kTileCols), 0, s, embed_grad, d, xs, skeys,
-                     batch_seq, vec);
-  ARK_HIP(hipGetLastError());
-  return ARK_OPT_OK;
+  return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws.p, L, s);
 }
 
 }  // extern "C"

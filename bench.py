@@ -400,15 +400,23 @@ def run_grad(a):
     tokens = torch.from_numpy(((rng.zipf(1.2, bs) - 1) % vocab).astype(np.int32)).cuda()
     dx0 = torch.randn(bs, d, device="cuda", generator=g)
     eg = dst[0].view(vocab, d)
-    for _ in range(a.warmup):
-        grad.embed_scatter(eg, tokens, dx0)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(a.steps):
-        grad.embed_scatter(eg, tokens, dx0)
-    e1.record()
-    torch.cuda.synchronize()
-    sc_ms = e0.elapsed_time(e1) / a.steps
+
+    def time_scatter(tok, rows):
+        for _ in range(a.warmup):
+            grad.embed_scatter(eg, tok, rows)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(a.steps):
+            grad.embed_scatter(eg, tok, rows)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / a.steps
+
+    sc_ms = time_scatter(tokens, dx0)
+    big = 4 * bs  # four tiles: the multi-block sort
+    tokens4 = torch.from_numpy(((rng.zipf(1.2, big) - 1) % vocab).astype(np.int32)).cuda()
+    dx4 = torch.randn(big, d, device="cuda", generator=g)
+    sc4_ms = time_scatter(tokens4, dx4)
     uniq = int(torch.unique(tokens).numel())
     cpu = None
     if not a.no_cpu:
@@ -436,7 +444,8 @@ def run_grad(a):
         "config": {"workload": "grad: 272 EKO-237M fp32 gradient buffers += backward outputs; "
                                "token scatter of 4096 tokens (Zipf 1.2) into 32000 x 768",
                    "elements": n, "bytes_per_launch": 12 * n,
-                   "scatter_ms": round(sc_ms, 4), "scatter_unique_tokens": uniq},
+                   "scatter_ms": round(sc_ms, 4), "scatter_unique_tokens": uniq,
+                   "scatter_16384_tokens_ms": round(sc4_ms, 4)},
         "roofline": {"kernel": "grad_batch", "bound": "hbm", "achieved": round(gbs, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": traffic_from_profiles("eko237m", "grad_batch")[0],

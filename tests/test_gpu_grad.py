@@ -33,11 +33,17 @@ def _zipf_tokens(rng, n, vocab, extra=0):
 @pytest.mark.parametrize("vocab,d,n,extra", [(32000, 768, 4096, 0), (32000, 768, 4096, 50),
                                              (1000, 33, 777, 10), (5, 64, 2000, 2),
                                              (32000, 768, 1, 0), (32768, 768, 4096, 0),
-                                             (32000, 768, 4097, 0), (32000, 256, 9000, 5)])
+                                             (32000, 768, 4097, 0), (32000, 768, 4146, 0),
+                                             (32000, 256, 9000, 5), (32000, 64, 8192, 0),
+                                             (256, 16, 12289, 3), (1, 8, 5000, 4),
+                                             (70000, 8, 20000, 100), (100000, 4, 70001, 0)])
 def test_scatter_matches_oracle(vocab, d, n, extra):
     """Up to 4096 tokens the positions are sorted by one block in LDS, past
-    that by the device-wide radix sort; vocab 32768 puts the largest real key
-    on the block sort's padding key."""
+    that by one hist/scan/scatter launch triple per 8-bit digit over
+    4096-token tiles: two tiles exactly (8192), a one-token last tile
+    (4097, 12289), one pass (vocab 256 and 1), two, and three (vocab 70000
+    and 100000 take 17 key bits); vocab 32768 puts the largest real key on
+    the block sort's padding key."""
     torch = _torch()
     rng = np.random.default_rng(vocab + d + n)
     tokens = _zipf_tokens(rng, n, vocab, extra)
@@ -68,6 +74,47 @@ def test_scatter_largest_key_ties_with_the_block_sort_padding():
     want = g.copy()
     oracle.embed_scatter(want, tokens, dx0)
     gg = torch.from_numpy(g).cuda()
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [4097, 8191, 8193])
+def test_scatter_largest_key_ties_with_the_last_tile_padding(n):
+    """Past one tile the last tile's positions beyond n carry the all-ones
+    key too; the real rows of token 32767 (the largest key over 15 bits)
+    spread over every tile must keep their order and land before it."""
+    torch = _torch()
+    vocab, d = 32768, 16
+    rng = np.random.default_rng(n)
+    tokens = rng.integers(0, vocab, n).astype(np.uint32)
+    tokens[::5] = vocab - 1
+    tokens[-3:] = vocab - 1
+    tokens[7] = vocab + 9  # out of range: row 0
+    dx0 = (rng.standard_normal((n, d)) * 10.0 ** rng.integers(-4, 4, (n, 1))).astype(np.float32)
+    g = rng.standard_normal((vocab, d)).astype(np.float32)
+    want = g.copy()
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.from_numpy(g).cuda()
+    grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
+                       torch.from_numpy(dx0).cuda())
+    np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
+
+
+def test_scatter_one_long_run_across_tiles():
+    """One token at all 10000 positions: a single run that the multi-tile
+    sort must keep in position order across three tiles, added with the
+    order-revealing values (1e8, 1, -1e8, 1) at the tile seams."""
+    torch = _torch()
+    vocab, d, n = 50, 64, 10000
+    rng = np.random.default_rng(17)
+    dx0 = rng.standard_normal((n, d)).astype(np.float32)
+    for seam in (4094, 8190):
+        dx0[seam:seam + 4, :] = np.array([1e8, 1.0, -1e8, 1.0], np.float32)[:, None]
+    tokens = np.full(n, 31, np.uint32)
+    want = np.zeros((vocab, d), np.float32)
+    oracle.embed_scatter(want, tokens, dx0)
+    gg = torch.zeros(vocab, d, device="cuda")
     grad.embed_scatter(gg, torch.from_numpy(tokens.view(np.int32)).cuda(),
                        torch.from_numpy(dx0).cuda())
     np.testing.assert_array_equal(_bits(gg).reshape(vocab, d), want.view(np.uint32))
