@@ -69,6 +69,7 @@ def _declare(L):
         "ark_grad_plan_run": ([H], C.c_int),
         "ark_grad_plan_destroy": ([H], C.c_int),
         "ark_grad_embed_scatter": ([P, u32, u32, P, P, u32, P], C.c_int),
+        "ark_grad_embed_scatter_noalloc": ([P, u32, u32, P, P, u32, P], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

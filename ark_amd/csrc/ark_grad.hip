@@ -29,6 +29,7 @@
 //       the CPU loop, and the result is bit-identical.
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "ark_common.hpp"
@@ -568,6 +569,44 @@ int scatter_launch(float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t
 
 }  // namespace
 
+// ---- the scatter's workspace without allocation --------------------------
+// One file-scope device array per GPU, held from the library's first use on
+// that GPU to the end of the process.  Host code never passes `scratch`
+// itself to a kernel (on the host the name is only a stand-in for the
+// symbol): it looks the array's device address up once per device with
+// hipGetSymbolAddress, with that device current, and uses that address.
+static __device__ __align__(256) uint8_t scratch[ARK_GRAD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of device dev's copy of scratch, looked up on the first call
+// for that device.
+int scratch_ptr(int dev, void** out) {
+  *out = nullptr;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ARK_OPT_EINVAL, "device %d out of range for the static scratch", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    ark::DeviceGuard g(dev);
+    if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", dev);
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return ark::hip_fail(e, "hipGetSymbolAddress(scratch)");
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ARK_OPT_OK;
+}
+
+}  // namespace
+
 struct ark_grad_plan {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -681,6 +720,30 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
     return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", L.bytes);
   }
   return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws.p, L, s);
+}
+
+int ark_grad_embed_scatter_noalloc(float* embed_grad, uint32_t vocab, uint32_t d,
+                                   const uint32_t* tokens, const float* dx0, uint32_t batch_seq,
+                                   void* stream) {
+  bool skip = false;
+  int rc = scatter_check(embed_grad, vocab, d, tokens, dx0, batch_seq, &skip);
+  if (rc || skip) return rc;
+  const ScatterLayout L = scatter_layout(batch_seq, d);
+  if (L.bytes > (size_t)ARK_GRAD_SCRATCH_BYTES)
+    return fail(ARK_OPT_EINVAL,
+                "scatter of %u tokens x %u columns needs %zu bytes of workspace; the static "
+                "scratch holds %llu (ark_grad_embed_scatter allocates instead)",
+                batch_seq, d, L.bytes, (unsigned long long)ARK_GRAD_SCRATCH_BYTES);
+  hipStream_t s = (hipStream_t)stream;
+  int dev = -1;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return ark::hip_fail(e, "device of the stream");
+  }
+  void* ws = nullptr;
+  if ((rc = scratch_ptr(dev, &ws))) return rc;
+  return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws, L, s);
 }
 
 }  // extern "C"

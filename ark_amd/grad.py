@@ -58,13 +58,15 @@ class GradPlan:
             pass
 
 
-def embed_scatter(embed_grad, tokens, dx0):
+def embed_scatter(embed_grad, tokens, dx0, noalloc=False):
     """embed_grad (vocab x d float32) += rows of dx0 (batch x d float32) at
-    the rows of tokens (int32/uint32, batch); tokens >= vocab go to row 0."""
-    import torch
+    the rows of tokens (int32/uint32, batch); tokens >= vocab go to row 0.
+    noalloc: use the entry point whose workspace is the library's static
+    device array instead of the stream-ordered pool."""
     _f32(embed_grad), _f32(dx0)
     assert tokens.is_cuda and tokens.is_contiguous() and tokens.element_size() == 4
     vocab, d = embed_grad.shape
     assert dx0.shape == (tokens.numel(), d)
-    check(lib().ark_grad_embed_scatter(embed_grad.data_ptr(), vocab, d, tokens.data_ptr(),
-                                       dx0.data_ptr(), tokens.numel(), _stream()))
+    fn = lib().ark_grad_embed_scatter_noalloc if noalloc else lib().ark_grad_embed_scatter
+    check(fn(embed_grad.data_ptr(), vocab, d, tokens.data_ptr(), dx0.data_ptr(), tokens.numel(),
+             _stream()))

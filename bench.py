@@ -401,18 +401,19 @@ def run_grad(a):
     dx0 = torch.randn(bs, d, device="cuda", generator=g)
     eg = dst[0].view(vocab, d)
 
-    def time_scatter(tok, rows):
+    def time_scatter(tok, rows, noalloc=False):
         for _ in range(a.warmup):
-            grad.embed_scatter(eg, tok, rows)
+            grad.embed_scatter(eg, tok, rows, noalloc=noalloc)
         torch.cuda.synchronize()
         e0.record()
         for _ in range(a.steps):
-            grad.embed_scatter(eg, tok, rows)
+            grad.embed_scatter(eg, tok, rows, noalloc=noalloc)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / a.steps
 
     sc_ms = time_scatter(tokens, dx0)
+    sc_na_ms = time_scatter(tokens, dx0, noalloc=True)
     big = 4 * bs  # four tiles: the multi-block sort
     tokens4 = torch.from_numpy(((rng.zipf(1.2, big) - 1) % vocab).astype(np.int32)).cuda()
     dx4 = torch.randn(big, d, device="cuda", generator=g)
@@ -445,6 +446,7 @@ def run_grad(a):
                                "token scatter of 4096 tokens (Zipf 1.2) into 32000 x 768",
                    "elements": n, "bytes_per_launch": 12 * n,
                    "scatter_ms": round(sc_ms, 4), "scatter_unique_tokens": uniq,
+                   "scatter_noalloc_ms": round(sc_na_ms, 4),
                    "scatter_16384_tokens_ms": round(sc4_ms, 4)},
         "roofline": {"kernel": "grad_batch", "bound": "hbm", "achieved": round(gbs, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),

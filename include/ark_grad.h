@@ -56,6 +56,30 @@ int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
                            const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                            void *stream);
 
+/* Size of the device array behind ark_grad_embed_scatter_noalloc: 48 MiB
+ * per GPU, held from the first call on that GPU until the process ends. */
+#define ARK_GRAD_SCRATCH_BYTES (48ull << 20)
+
+/* ark_grad_embed_scatter with the same arguments and bit-identical results,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Its workspace is a static device array of
+ * ARK_GRAD_SCRATCH_BYTES per GPU instead of the stream-ordered pool, so it
+ * calls no hipMalloc, hipFree or other allocating routine (the first call on
+ * a GPU looks the array's address up once).  The workspace is
+ *   8 * batch_seq bytes, plus 8 * batch_seq + 1024 * ceil(batch_seq / 4096)
+ *   more when batch_seq > 4096, plus 4 * batch_seq * d,
+ * each part rounded up to 256 bytes (a 2 x 2048-token batch at d = 768
+ * needs 12.6 MB, at d = 2048 33.6 MB); a larger one is rejected with
+ * ARK_OPT_EINVAL before anything is queued.  Every call on a GPU shares that
+ * GPU's array, and each call writes every workspace byte it reads, so
+ * nothing carries over from the previous call; calls that overlap on one
+ * GPU (two streams, or two host threads) race on the array and must be
+ * serialised by the caller. */
+int ark_grad_embed_scatter_noalloc(float *embed_grad, uint32_t vocab, uint32_t d,
+                                   const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
+                                   void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -138,6 +138,9 @@ def test_next_rows_reject_bad_arguments_before_device_calls():
     assert L.ark_grad_accumulate(6, 8, 4, None) == _abi.EINVAL and "aligned" in msg()
     assert L.ark_grad_embed_scatter(None, 0, 4, None, None, 3, None) == _abi.EINVAL and "vocab" in msg()
     assert L.ark_grad_embed_scatter(None, 10, 4, None, None, 0, None) == 0  # empty batch
+    assert (L.ark_grad_embed_scatter_noalloc(None, 0, 4, None, None, 3, None) == _abi.EINVAL
+            and "vocab" in msg())
+    assert L.ark_grad_embed_scatter_noalloc(None, 10, 4, None, None, 0, None) == 0
     recs = (_abi.CkptRecord * 1)()
     recs[0] = _abi.CkptRecord(0, 4, 9, 0)
     out = C.c_uint64()
