@@ -113,9 +113,9 @@ __global__ __launch_bounds__(kWave) void grad_batch(const GradSeg* __restrict__ 
 // (wave, item, lane) is the position order.  One pass sorts the tile by
 // kRadixBits bits of the key:
 //   rank   per item, how many items of its wave with the same digit precede
-//          it, from ballots of the digit's bits (wave_rank); the digit's
-//          last item in the wave also writes the wave's count of it into an
-//          LDS table laid out digit-major, (digit, wave);
+//          it, from ballots of the digit's bits and the wave's running count
+//          of each digit in LDS (wave_rank), which ends as the (digit, wave)
+//          count table;
 //   scan   an exclusive block scan of that table gives every (digit, wave)
 //          the number of tile items before it in (digit, position) order;
 //   place  item -> scan[digit, wave] + rank.
@@ -147,40 +147,39 @@ __device__ __forceinline__ uint32_t tile_pos(uint32_t wave, int j, uint32_t lane
   return wave * (kSortItems * kWave) + (uint32_t)j * kWave + lane;
 }
 
+// The (digit, wave) table in LDS: wave w's counter of digit d at
+// w * kHistStride + d; the stride of kRadix + 1 words puts the counters of
+// different digits of one wave in different banks.
+constexpr uint32_t kHistStride = kRadix + 1;
+constexpr uint32_t kHistWords = kSortWaves * kHistStride;
+__device__ __forceinline__ uint32_t hist_at(uint32_t d, uint32_t w) { return w * kHistStride + d; }
+
 // rank[j] = the number of items of this wave with digit dig[j] that precede
-// item j in (item, lane) order.  The last such item of each digit writes the
-// wave's count of the digit to hist[digit * kSortWaves + wave]; entries of
-// digits absent from the wave are left as they are (zero).
+// item j in (item, lane) order; on return the wave's counters hold its count
+// of every digit.  Round j matches item j's digit across the lanes with
+// kRadixBits ballots, adds the wave's running count of that digit, and the
+// digit's last lane in the round writes the new count.  A round's reads all
+// come before its writes (one wave, LDS accesses in program order), and
+// different waves touch different counters.
 __device__ __forceinline__ void wave_rank(const uint32_t (&dig)[kSortItems],
                                           uint32_t (&rank)[kSortItems], uint32_t* hist,
                                           uint32_t wave) {
   const uint32_t lane = __lane_id();
   const uint64_t below = (1ull << lane) - 1ull;
   const uint64_t above = ~((2ull << lane) - 1ull);  // lane 63: 2 << 63 wraps to 0
-  uint64_t bal[kSortItems][kRadixBits];
-#pragma unroll
-  for (int i = 0; i < kSortItems; ++i)
-#pragma unroll
-    for (int b = 0; b < kRadixBits; ++b) bal[i][b] = __ballot((dig[i] >> b) & 1u);
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
-    uint64_t same[kSortItems];  // lanes whose item i has digit dig[j]
+    uint64_t same = ~0ull;  // lanes whose item j has digit dig[j]
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-      uint64_t m = ~0ull;
-#pragma unroll
-      for (int b = 0; b < kRadixBits; ++b) m &= ((dig[j] >> b) & 1u) ? bal[i][b] : ~bal[i][b];
-      same[i] = m;
+    for (int b = 0; b < kRadixBits; ++b) {
+      const uint32_t bit = (dig[j] >> b) & 1u;
+      const uint64_t ones = __ballot(bit);
+      same &= bit ? ones : ~ones;
     }
-    uint32_t r = (uint32_t)__popcll(same[j] & below);
-    bool last = (same[j] & above) == 0ull;
-#pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-      if (i < j) r += (uint32_t)__popcll(same[i]);
-      if (i > j) last = last && same[i] == 0ull;
-    }
+    uint32_t* c = hist + hist_at(dig[j], wave);
+    const uint32_t r = *c + (uint32_t)__popcll(same & below);
     rank[j] = r;
-    if (last) hist[dig[j] * kSortWaves + wave] = r + 1u;
+    if ((same & above) == 0ull) *c = r + 1u;
   }
 }
 
@@ -219,23 +218,26 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t (&e)[4], uint32_t* 
 }
 
 // One pass of the tile in registers: zero the (digit, wave) table, rank,
-// scan.  On return hist[d * kSortWaves + w] holds the number of tile items
+// scan.  On return hist[hist_at(d, w)] holds the number of tile items
 // (padding included) before (digit d, wave w) in (digit, position) order.
 __device__ __forceinline__ void tile_pass(const uint32_t (&dig)[kSortItems],
                                           uint32_t (&rank)[kSortItems], uint32_t* hist,
                                           uint32_t* wsum) {
   const uint32_t t = threadIdx.x, wave = t / kWave;
+  // thread t scans entries 4t .. 4t+3 of the (digit, wave) order: digit
+  // t / 4, waves 4 (t % 4) .. 4 (t % 4) + 3
+  const uint32_t sd = t / 4u, sw = 4u * (t % 4u);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hist[4 * t + i] = 0u;
+  for (int i = 0; i < 4; ++i) hist[hist_at(sd, sw + i)] = 0u;
   __syncthreads();
   wave_rank(dig, rank, hist, wave);
   __syncthreads();
   uint32_t e[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) e[i] = hist[4 * t + i];
+  for (int i = 0; i < 4; ++i) e[i] = hist[hist_at(sd, sw + i)];
   block_exclusive(e, wsum, 0u);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hist[4 * t + i] = e[i];
+  for (int i = 0; i < 4; ++i) hist[hist_at(sd, sw + i)] = e[i];
   __syncthreads();
 }
 
@@ -246,7 +248,8 @@ __device__ __forceinline__ void tile_pass(const uint32_t (&dig)[kSortItems],
 __global__ __launch_bounds__(kSortThreads) void block_sort_kernel(
     const uint32_t* __restrict__ tokens, uint32_t n, uint32_t vocab, int end_bit,
     uint32_t* __restrict__ skeys, uint32_t* __restrict__ svals) {
-  __shared__ uint32_t s_keys[kSortTile], s_vals[kSortTile], s_hist[kHist], s_wsum[kSortWaves];
+  __shared__ uint32_t s_keys[kSortTile], s_vals[kSortTile], s_hist[kHistWords],
+      s_wsum[kSortWaves];
   const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
   uint32_t k[kSortItems], v[kSortItems], dg[kSortItems], r[kSortItems];
 #pragma unroll
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(kSortThreads) void block_sort_kernel(
     tile_pass(dg, r, s_hist, s_wsum);
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
-      const uint32_t dst = s_hist[dg[j] * kSortWaves + wave] + r[j];
+      const uint32_t dst = s_hist[hist_at(dg[j], wave)] + r[j];
       s_keys[dst] = k[j];
       s_vals[dst] = v[j];
     }
@@ -284,24 +287,42 @@ __global__ __launch_bounds__(kSortThreads) void block_sort_kernel(
 }
 
 // counts[d * tiles + tile] = the items of the tile whose key has digit d at
-// this pass.  from_tokens: the keys are the clamped tokens (first pass).
+// this pass: the waves' counters of wave_rank, summed over the waves.
+// from_tokens: the keys are the clamped tokens (first pass).  Positions past
+// n count as the padding digit, which sort_scatter_kernel never places, and
+// are taken off again.
 __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(
     const uint32_t* __restrict__ keys, uint32_t from_tokens, uint32_t n, uint32_t vocab,
     int shift, uint32_t* __restrict__ counts, uint32_t tiles) {
-  __shared__ uint32_t h[kRadix];
-  if (threadIdx.x < kRadix) h[threadIdx.x] = 0u;
-  __syncthreads();
+  __shared__ uint32_t s_hist[kHistWords];
+  const uint32_t t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+  const uint32_t sd = t / 4u, sw = 4u * (t % 4u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_hist[hist_at(sd, sw + i)] = 0u;
+  uint32_t dg[kSortItems], r[kSortItems];
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
-    const uint32_t p = blockIdx.x * kSortTile + (uint32_t)j * kSortThreads + threadIdx.x;
+    const uint32_t p = blockIdx.x * kSortTile + tile_pos(wave, j, lane);
+    uint32_t key = kPadKey;
     if (p < n) {
-      uint32_t key = ld_g<uint32_t>(keys + p);
+      key = ld_g<uint32_t>(keys + p);
       if (from_tokens) key = clamp_token(key, vocab);
-      atomicAdd(&h[(key >> shift) & (kRadix - 1u)], 1u);
     }
+    dg[j] = (key >> shift) & (kRadix - 1u);
   }
   __syncthreads();
-  if (threadIdx.x < kRadix) counts[threadIdx.x * tiles + blockIdx.x] = h[threadIdx.x];
+  wave_rank(dg, r, s_hist, wave);
+  __syncthreads();
+  if (t < kRadix) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) c += s_hist[hist_at(t, w)];
+    if (t == kRadix - 1u) {  // the padding: only the last tile has any
+      const uint64_t end = (uint64_t)(blockIdx.x + 1) * kSortTile;
+      c -= end > n ? (uint32_t)(end - n) : 0u;
+    }
+    counts[t * tiles + blockIdx.x] = c;
+  }
 }
 
 // counts[0, total) <- its exclusive prefix sums: one block, kSortTile
@@ -336,7 +357,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     uint32_t from_tokens, uint32_t n, uint32_t vocab, int shift,
     const uint32_t* __restrict__ counts, uint32_t tiles, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out) {
-  __shared__ uint32_t s_hist[kHist], s_wsum[kSortWaves];
+  __shared__ uint32_t s_hist[kHistWords], s_wsum[kSortWaves];
   const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave, tile = blockIdx.x;
   uint32_t k[kSortItems], v[kSortItems], dg[kSortItems], r[kSortItems];
 #pragma unroll
@@ -362,7 +383,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     if (p < n) {
       const uint32_t d = dg[j];
       const uint32_t dst = counts[d * tiles + tile] +
-                           (s_hist[d * kSortWaves + wave] - s_hist[d * kSortWaves]) + r[j];
+                           (s_hist[hist_at(d, wave)] - s_hist[hist_at(d, 0)]) + r[j];
       keys_out[dst] = k[j];
       vals_out[dst] = v[j];
     }
