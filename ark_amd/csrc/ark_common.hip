@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <string>
 
 namespace ark {
@@ -95,6 +96,32 @@ int BufferChecker::check(const void* p, uint64_t bytes, const char* what, int id
     if (used_ < kRanges) ++used_;
   }
   return rc;
+}
+
+int check_disjoint(std::vector<Span> written, std::vector<Span> readonly) {
+  auto empty = [](const Span& x) { return x.hi <= x.lo; };
+  written.erase(std::remove_if(written.begin(), written.end(), empty), written.end());
+  readonly.erase(std::remove_if(readonly.begin(), readonly.end(), empty), readonly.end());
+  auto by_lo = [](const Span& a, const Span& b) { return a.lo < b.lo; };
+  std::sort(written.begin(), written.end(), by_lo);
+  // sorted by start, no two overlap iff each starts at or past the previous
+  // one's end
+  for (size_t i = 1; i < written.size(); ++i) {
+    const Span &a = written[i - 1], &b = written[i];
+    if (b.lo < a.hi)
+      return fail(ARK_OPT_EINVAL, "tensor %d %s overlaps tensor %d %s (both written)", a.idx,
+                  a.what, b.idx, b.what);
+  }
+  // disjoint and sorted: the ends are sorted too, so the first written span
+  // ending past r.lo is the only candidate for overlapping r
+  for (const Span& r : readonly) {
+    auto it = std::upper_bound(written.begin(), written.end(), r.lo,
+                               [](uintptr_t x, const Span& s) { return x < s.hi; });
+    if (it != written.end() && it->lo < r.hi)
+      return fail(ARK_OPT_EINVAL, "tensor %d %s overlaps tensor %d %s (written by the step)",
+                  r.idx, r.what, it->idx, it->what);
+  }
+  return ARK_OPT_OK;
 }
 
 DeviceGuard::DeviceGuard(int dev) {

@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "ark_opt.h"
 
 namespace ark {
@@ -56,6 +58,19 @@ inline bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bby
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
   return x < y + bbytes && y < x + abytes;
 }
+
+// A byte range [lo, hi) of a caller buffer, named for error messages.
+struct Span {
+  uintptr_t lo = 0, hi = 0;
+  const char* what = "";
+  int idx = 0;
+};
+
+// Fails with ARK_OPT_EINVAL, naming both buffers, when two written spans
+// share a byte or a read-only span shares a byte with a written one (read-
+// only spans may overlap each other).  Empty spans are ignored.  Host-only:
+// compares addresses, queries nothing.
+int check_disjoint(std::vector<Span> written, std::vector<Span> readonly);
 
 // Scratch device memory from the stream-ordered pool, freed in stream order
 // when the owner goes out of scope (after the work queued on it).

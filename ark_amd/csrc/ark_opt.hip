@@ -200,6 +200,28 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   if (parts > ark::kMaxParts)
     return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
 
+  // The reference steps distinct per-tensor fields (optimizer.rs:171,
+  // memory.rs:202-255), so w, m and v can never alias.  Here a tensor listed
+  // twice or overlapping buffers would have two waves rewrite the same
+  // words: refuse any written span shared with another written span or with
+  // a gradient.
+  {
+    std::vector<ark::Span> written, grads;
+    written.reserve(3 * (size_t)n_tensors);
+    grads.reserve((size_t)n_tensors);
+    for (int32_t i = 0; i < n_tensors; ++i) {
+      const ark_opt_tensor& t = tensors[i];
+      if (t.n == 0) continue;
+      const uintptr_t w = (uintptr_t)t.w, g = (uintptr_t)t.g, m = (uintptr_t)t.m,
+                      v = (uintptr_t)t.v;
+      written.push_back({w, w + t.n * 2u, "w", i});
+      written.push_back({m, m + t.n * 4u, "m", i});
+      written.push_back({v, v + t.n * 4u, "v", i});
+      grads.push_back({g, g + t.n * gsz, "g", i});
+    }
+    if ((rc = ark::check_disjoint(std::move(written), std::move(grads)))) return rc;
+  }
+
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
   ark::BufferChecker checker;
@@ -421,6 +443,11 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   if (n > (1ull << 48) || (n + ark::kRow - 1) / ark::kRow * 64u >= (1ull << 32))
     return fail(ARK_OPT_EINVAL, "n too large (%llu)", (unsigned long long)n);
   int rc;
+  const uintptr_t uw = (uintptr_t)w, ug = (uintptr_t)g, um = (uintptr_t)m, uv = (uintptr_t)v;
+  if ((rc = ark::check_disjoint({{uw, uw + n * 2u, "w", 0}, {um, um + n * 4u, "m", 0},
+                                 {uv, uv + n * 4u, "v", 0}},
+                                {{ug, ug + n * 4u, "g", 0}})))
+    return rc;
   if ((rc = check_buffer(w, n * 2u, "w", 0))) return rc;
   if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
   if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;

@@ -156,7 +156,12 @@ int ark_opt_default_hparams(ark_opt_hparams *out);
 /* Optimizer::new (optimizer.rs:74) over a parameter-buffer set.  Copies the
  * table and its segment map to the device, allocates the workspace and the
  * device state (t = 0, loss_scale = loss_scale_init), and binds the handle to
- * `stream` on the current device.  One handle per stream; not thread safe. */
+ * `stream` on the current device.  One handle per stream; not thread safe.
+ * The buffers the step writes (every tensor's w, m and v) must be pairwise
+ * disjoint and disjoint from every g, as the reference's distinct per-tensor
+ * fields are (memory.rs:202-255); a table that lists a tensor twice or
+ * overlaps them is refused with ARK_OPT_EINVAL.  Gradients may overlap each
+ * other (they are only read). */
 int ark_opt_create(const ark_opt_tensor *tensors, int32_t n_tensors,
                    const ark_opt_hparams *hp, void *stream,
                    ark_opt_handle **out);
@@ -193,7 +198,8 @@ int ark_opt_get_timing(ark_opt_handle *h, ark_opt_timing *out);
  * order, fp32 gradients used as given (no unscale, no clip), t == 0 treated
  * as 1, plus the stream.  Runs the same per-row AdamW code as ark_opt_step
  * over the one tensor, with the step scalars passed as kernel arguments
- * (no table upload, nothing allocated); returns once the work is queued. */
+ * (no table upload, nothing allocated); returns once the work is queued.
+ * w, m, v and g must not share a byte (ARK_OPT_EINVAL otherwise). */
 int ark_hip_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
                           uint64_t n, float lr, float beta1, float beta2,
                           float eps, float wd, uint32_t t, void *stream);

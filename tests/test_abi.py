@@ -81,6 +81,62 @@ def test_create_rejects_bad_arguments_before_device_calls():
         assert rc == _abi.EINVAL and "too large" in msg, (n, msg)
 
 
+def _table(rows):
+    """A tensor table of fake device addresses: rows of (w, g, m, v, n)."""
+    t = (_abi.Tensor * len(rows))()
+    for i, (w, g, m, v, n) in enumerate(rows):
+        t[i].w, t[i].g, t[i].m, t[i].v, t[i].n = w, g, m, v, n
+    return t
+
+
+MB = 1 << 20
+
+
+def test_create_rejects_aliased_buffers_before_device_calls():
+    """The reference steps distinct per-tensor fields (optimizer.rs:171,
+    memory.rs:202-255); a table whose written buffers (w, m, v) share a byte
+    with each other or with a gradient is refused, naming both, before any
+    device query (the addresses here are not memory at all)."""
+    ok = [(1 * MB, 2 * MB, 3 * MB, 4 * MB, 1000), (5 * MB, 6 * MB, 7 * MB, 8 * MB, 1000)]
+    cases = {
+        "duplicate entry": ([ok[0], ok[1], ok[0]], ["tensor 0 w", "tensor 2 w"]),
+        "partial w overlap": ([ok[0], (1 * MB + 1998, 6 * MB, 7 * MB, 8 * MB, 1000)],
+                              ["tensor 0 w", "tensor 1 w"]),
+        "m equal to v": ([ok[0], (5 * MB, 6 * MB, 7 * MB, 7 * MB, 1000)],
+                         ["tensor 1 m", "tensor 1 v"]),
+        "g inside w": ([(1 * MB, 1 * MB + 400, 3 * MB, 4 * MB, 1000), ok[1]],
+                       ["tensor 0 g", "tensor 0 w"]),
+        "g of one tensor on another's v": ([ok[0], (5 * MB, 4 * MB + 3996, 7 * MB, 8 * MB, 1000)],
+                                           ["tensor 1 g", "tensor 0 v"]),
+    }
+    for name, (rows, words) in cases.items():
+        rc, h, msg = _create(_table(rows), len(rows), _hp())
+        assert rc == _abi.EINVAL and not h.value, (name, msg)
+        assert "overlaps" in msg and all(w in msg for w in words), (name, msg)
+    # touching but disjoint spans, an empty tensor on top of another and two
+    # tensors sharing one read-only gradient pass the check (and then fail the
+    # device query, since the addresses are fake)
+    for rows in ([(1 * MB, 2 * MB, 3 * MB, 4 * MB, 1000), (1 * MB + 2000, 2 * MB, 3 * MB + 4000,
+                                                           4 * MB + 4000, 1000)],
+                 [ok[0], (1 * MB, 1 * MB, 1 * MB, 1 * MB, 0)]):
+        rc, h, msg = _create(_table(rows), len(rows), _hp())
+        assert rc != _abi.OK and "overlaps" not in msg, msg
+
+
+def test_single_tensor_dropin_rejects_aliased_buffers():
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    args = (3e-4, 0.9, 0.999, 1e-8, 0.01, 1, None)
+    for (w, g, m, v), words in [((1 * MB, 2 * MB, 3 * MB, 3 * MB), ("m", "v")),
+                                ((1 * MB, 1 * MB + 8, 3 * MB, 4 * MB), ("g", "w")),
+                                ((1 * MB, 2 * MB, 1 * MB + 1996, 4 * MB), ("w", "m")),
+                                ((1 * MB, 4 * MB + 3996, 3 * MB, 4 * MB), ("g", "v"))]:
+        assert L.ark_hip_adam_step_f16(w, g, m, v, 1000, *args) == _abi.EINVAL
+        assert "overlaps" in msg() and all(f"0 {x}" in msg() for x in words), msg()
+    assert L.ark_hip_adam_step_f16(1 * MB, 2 * MB, 3 * MB, 3 * MB + 4000, 1000, *args) != 0
+    assert "overlaps" not in msg()
+
+
 def test_single_tensor_dropin_argument_checks():
     L = _lib.lib()
     assert L.ark_hip_adam_step_f16(None, None, None, None, 0, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1,
