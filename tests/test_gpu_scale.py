@@ -2,6 +2,7 @@
 (c2), its 5000-step AMP stress trajectory (c3) and the 1.3B scale-up (c4),
 checked against the CPU oracle bit for bit (every scalar and every w/m/v
 element of the steps run), plus the state/restore and timing entry points."""
+import ctypes as C
 import os
 
 import numpy as np
@@ -25,18 +26,21 @@ def _opt(ps, scale, **amp_kw):
     return cfg, Optimizer(cfg, ps, amp)
 
 
-def _full_size_steps(name, sig, scale, steps, seed):
+def _full_size_steps(name, sig, scale, steps, seed, sig_at=None):
+    """steps fresh-gradient steps on the GPU and the oracle, every scalar and
+    every w/m/v element compared after each; sig_at(k) gives step k's
+    per-tensor sigmas (default: sig throughout)."""
     specs = config_tensors(name)
-    from ark_amd.optimizer import AdamConfig
-    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, scale)
+    sig_at = sig_at or (lambda k: sig)
+    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig_at(0), scale)
     cfg, opt = _opt(ps, scale)
-    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, scale, nthreads=THREADS)
+    ts = H.host_problem(specs, seed, HP["weight_decay"], sig_at(0), scale, nthreads=THREADS)
     ref = oracle.Optimizer(ts, opt.hp, nthreads=THREADS)
     infos = []
     for k in range(steps):
         if k:
-            H.gpu_regen_grads(ps, seed, sig, scale, k)
-            H.host_regen_grads(ts, seed, sig, scale, k, nthreads=THREADS)
+            H.gpu_regen_grads(ps, seed, sig_at(k), scale, k)
+            H.host_regen_grads(ts, seed, sig_at(k), scale, k, nthreads=THREADS)
         _, gi = opt.step_all(cfg.lr, info=True)
         _, ri = ref.step(cfg.lr)
         assert not H.info_matches(gi, ri), (k, H.info_matches(gi, ri))
@@ -54,6 +58,25 @@ def test_config2_eko237m_full_size_bit_exact():
     sig = H.log_uniform_sigmas(len(specs), 20260501)
     infos = _full_size_steps("c2", sig, 65536.0, 2, 20260501)
     assert all(i.applied for i in infos) and infos[-1].state.t == 2
+
+
+def test_config2_full_size_both_clip_branches():
+    """BASELINE c2's sigma = 10^U(-5,-2) gives a global norm of about 35.8, so
+    every c2 step clips.  The same 272-tensor set with those sigmas scaled to
+    put the norm at 0.9, 1.1 and 0.95 x grad_clip on three fresh-gradient
+    steps takes both branches of optimizer.rs:145-149 (unclipped, clipped,
+    unclipped) at full size, every element compared with the oracle."""
+    specs = config_tensors("c2")
+    base = H.log_uniform_sigmas(len(specs), 20260501)
+    est = float(np.sqrt(sum(s.n * float(x) ** 2 for s, x in zip(specs, base))))
+    assert 30.0 < est < 40.0, est
+    factors = [0.9, 1.1, 0.95]
+    sigs = [[float(x) * f / est for x in base] for f in factors]
+    infos = _full_size_steps("c2", None, 65536.0, 3, 20260502, sig_at=lambda k: sigs[k])
+    assert [i.applied for i in infos] == [1, 1, 1]
+    assert [i.clipped for i in infos] == [0, 1, 0], [i.grad_norm for i in infos]
+    for i, f in zip(infos, factors):
+        assert abs(i.grad_norm / HP["grad_clip"] - f) < 0.02, (i.grad_norm, f)
 
 
 def test_config4_scaleup_full_size_bit_exact():
@@ -166,16 +189,49 @@ def test_many_handles_create_and_destroy():
         opt.close()
 
 
+def _loaded_hip_runtime():
+    """The HIP runtime this process already uses (torch's), by the path it was
+    loaded from, so that dlopen returns that same library."""
+    import torch
+    torch.cuda.init()
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64.so" in ln}
+    assert len(paths) == 1, paths
+    hip = C.CDLL(paths.pop())
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipFree.argtypes = [C.c_void_p]
+    return hip
+
+
 def test_create_rejects_short_or_host_buffers():
     import torch
     from ark_amd._lib import ArkOptError
     from ark_amd.optimizer import AdamConfig, Optimizer, ParamSet
     specs = config_tensors("c0")
     ps = ParamSet(specs, 0.1)
-    tab = ps.table()
-    tab[0].n = 1 << 30  # 2 GiB of fp16: beyond the arena's allocation
-    with pytest.raises(ArkOptError, match="exceeds its allocation"):
-        Optimizer(AdamConfig(), ps, table=tab)
+    # A 16-element tensor whose w starts 16 bytes before the end of a 2 MiB
+    # hipMalloc allocation (not torch's, whose cached segments can be larger
+    # than the tensor), so it runs 16 bytes past it; its g, m and v sit
+    # 512 KiB into their arenas, where that overrun cannot reach (the spans
+    # are disjoint, so only the allocation check can refuse it).
+    hip = _loaded_hip_runtime()
+    tail = C.c_void_p()
+    assert hip.hipMalloc(C.byref(tail), C.c_size_t(2 << 20)) == 0
+    try:
+        off = 512 << 10
+        tab = (_abi.Tensor * 1)()
+        tab[0].w = tail.value + (2 << 20) - 16
+        tab[0].g = ps.g(0).data_ptr() + off
+        tab[0].m = ps.m(0).data_ptr() + off
+        tab[0].v = ps.v(0).data_ptr() + off
+        tab[0].n = 16
+        with pytest.raises(ArkOptError, match="w .*exceeds its allocation"):
+            Optimizer(AdamConfig(), ps, table=tab)
+        tab[0].w = tail.value
+        Optimizer(AdamConfig(), ps, table=tab).close()  # the same table in bounds is accepted
+    finally:
+        torch.cuda.synchronize()
+        assert hip.hipFree(tail) == 0
     host = np.zeros(16, np.float32)
     tab = ps.table()
     tab[0].m = host.ctypes.data
