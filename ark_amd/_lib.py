@@ -70,6 +70,8 @@ def _declare(L):
         "ark_grad_plan_destroy": ([H], C.c_int),
         "ark_grad_embed_scatter": ([P, u32, u32, P, P, u32, P], C.c_int),
         "ark_grad_embed_scatter_noalloc": ([P, u32, u32, P, P, u32, P], C.c_int),
+        "ark_grad_plan_run_final": ([H, H], C.c_int),
+        "ark_grad_embed_scatter_final": ([P, u32, u32, P, P, u32, H], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -35,6 +35,7 @@
 #include "ark_common.hpp"
 #include "ark_device.hpp"
 #include "ark_grad.h"
+#include "ark_opt_internal.hpp"
 
 namespace {
 
@@ -105,6 +106,106 @@ __global__ __launch_bounds__(kWave) void grad_batch(const GradSeg* __restrict__ 
     for (int j = 0; j < kPerLane; ++j)
       if (e0 + j < d.n) add1(d.dst + e0 + j, d.src + e0 + j);
   }
+}
+
+// ---- the norm's units from the kernels that finish the gradients ----------
+// (ark_opt_internal.hpp).  A unit is 256 consecutive elements of an
+// optimizer segment; its value is the pairwise f64 tree of the squares of the
+// unscaled gradients (zero past the segment's end), NaN if one of them is inf
+// or NaN.  Lane l of a wave holds elements [4l, 4l + 4) of the unit: the
+// pair sums of its quad, then the lanes in lane order.
+
+// The unit of the wave's four-per-lane values x (0 past the end), unscaled
+// by inv; written by lane 0.
+__device__ __forceinline__ void store_unit(const float (&x)[kPerLane], float inv, double* unit) {
+  uint32_t bad = 0;
+  double q[kPerLane];
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    bad |= (__float_as_uint(x[j]) & 0x7F800000u) == 0x7F800000u ? 1u : 0u;
+    const float gu = x[j] * inv;
+    q[j] = (double)gu * (double)gu;
+  }
+  double sum = (q[0] + q[1]) + (q[2] + q[3]);
+#pragma unroll
+  for (int st = 0; st < 6; ++st) sum = sum + __shfl_xor(sum, 1 << st);
+  const bool any_bad = __ballot(bad) != 0ull;
+  if (threadIdx.x == 0) *unit = any_bad ? __builtin_nan("") : sum;
+}
+
+// 1 / loss_scale (training.rs:244) unless the tensor keeps its scale.
+__device__ __forceinline__ float unit_inv(const ark_opt_state* state, uint32_t seg_flags) {
+  return (seg_flags & ark::kSegNoUnscale) ? 1.0f : 1.0f / state->loss_scale;
+}
+
+// grad_batch's add (same blocks, same accesses) plus the unit of the 256
+// elements each wave finishes: the final accumulation before a step.  The
+// plan's segments are the optimizer handle's, one for one.  (Writing the
+// gradients the step's AdamW pass reads first with cache-allocating stores,
+// last segment first, measured no faster: the pass gained nothing from them,
+// unlike from the norm pass's cache-allocating loads.)
+__global__ __launch_bounds__(kWave) void grad_batch_units(const GradSeg* __restrict__ segs,
+                                                          const ark::SegDesc* __restrict__ osegs,
+                                                          const ark_opt_state* __restrict__ state,
+                                                          double* __restrict__ units) {
+  const uint32_t s = blockIdx.x / kBlocksPerSeg, r = blockIdx.x % kBlocksPerSeg;
+  const GradSeg d = segs[s];
+  if (r * (uint32_t)(kWave * kPerLane) >= d.n) return;  // the unit lies past the end
+  const uint32_t e0 = (r * kWave + threadIdx.x) * kPerLane;
+  float x[kPerLane] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (d.vec && e0 + kPerLane <= d.n) {
+    f32x4 a = ld_nt<f32x4>(d.dst + e0);
+    const f32x4 b = ld_nt<f32x4>(d.src + e0);
+    a.x = a.x + b.x;
+    a.y = a.y + b.y;
+    a.z = a.z + b.z;
+    a.w = a.w + b.w;
+    st_nt<f32x4>(d.dst + e0, a);
+    x[0] = a.x;
+    x[1] = a.y;
+    x[2] = a.z;
+    x[3] = a.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      if (e0 + j < d.n) {
+        const float v = ld_g<float>(d.dst + e0 + j) + ld_g<float>(d.src + e0 + j);
+        st_g<float>(d.dst + e0 + j, v);
+        x[j] = v;
+      }
+    }
+  }
+  store_unit(x, unit_inv(state, osegs[s].flags), units + (uint64_t)s * kBlocksPerSeg + r);
+}
+
+// After the scatter's run_kernel: the unit of every (embedding row, 256-column
+// tile) the scatter changed, from the row's final values.  d % 256 == 0, so a
+// tile is one unit: row t, tile c is the tensor's unit t * (d / 256) + c.  One
+// wave per (sorted position, tile); positions that do not start a run exit.
+__global__ __launch_bounds__(kWave) void units_rows_kernel(const float* __restrict__ g, uint32_t d,
+                                                           const uint32_t* __restrict__ skeys,
+                                                           uint32_t vec,
+                                                           const ark_opt_state* __restrict__ state,
+                                                           uint32_t seg_flags,
+                                                           double* __restrict__ units) {
+  const uint32_t p = blockIdx.x;
+  const uint32_t t = skeys[p];
+  if (p > 0 && skeys[p - 1] == t) return;
+  const uint32_t c0 = blockIdx.y * kTileCols + threadIdx.x * kPerLane;
+  const float* gp = g + (uint64_t)t * d + c0;
+  float x[kPerLane];
+  if (vec) {
+    const f32x4 a = ld_g<f32x4>(gp);
+    x[0] = a.x;
+    x[1] = a.y;
+    x[2] = a.z;
+    x[3] = a.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) x[j] = ld_g<float>(gp + j);
+  }
+  store_unit(x, unit_inv(state, seg_flags),
+             units + (uint64_t)t * (d / kTileCols) + blockIdx.y);
 }
 
 // ---- stable LSD radix sort of (clamped token, position) ------------------
@@ -633,6 +734,8 @@ struct ark_grad_plan {
   hipStream_t stream = nullptr;
   uint32_t nseg = 0;
   GradSeg* d_segs = nullptr;
+  std::vector<const float*> span_dst;  // the spans as given, for matching an
+  std::vector<uint64_t> span_n;        // optimizer table
 };
 
 extern "C" {
@@ -689,6 +792,10 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
   ark_grad_plan* p = new ark_grad_plan();
   p->stream = (hipStream_t)stream;
   p->nseg = (uint32_t)segs.size();
+  for (int32_t i = 0; i < n_spans; ++i) {
+    p->span_dst.push_back(spans[i].dst);
+    p->span_n.push_back(spans[i].n);
+  }
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess && !segs.empty()) {
     e = hipMalloc(&p->d_segs, segs.size() * sizeof(GradSeg));
@@ -712,6 +819,28 @@ int ark_grad_plan_run(ark_grad_plan* p) {
   hipLaunchKernelGGL(grad_batch, dim3(p->nseg * kBlocksPerSeg), dim3(kWave), 0, p->stream,
                      p->d_segs);
   ARK_HIP(hipGetLastError());
+  return ARK_OPT_OK;
+}
+
+int ark_grad_plan_run_final(ark_grad_plan* p, ark_opt_handle* opt) {
+  if (!p) return fail(ARK_OPT_EINVAL, "plan is NULL");
+  ark::OptUnits U;
+  int rc = ark::opt_units_for_spans(opt, p->span_dst.data(), p->span_n.data(),
+                                    p->span_n.size(), &U);
+  if (rc) return rc;
+  if (U.stream != p->stream || U.device != p->device)
+    return fail(ARK_OPT_EINVAL, "the plan and the optimizer handle must share a stream");
+  if (U.nseg != p->nseg)
+    return fail(ARK_OPT_EINVAL, "plan and optimizer table differ in segments (%u, %u)", p->nseg,
+                U.nseg);
+  if (p->nseg) {
+    ark::DeviceGuard g(p->device);
+    if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
+    hipLaunchKernelGGL(grad_batch_units, dim3(p->nseg * kBlocksPerSeg), dim3(kWave), 0,
+                       p->stream, p->d_segs, U.segs, U.state, U.units);
+    ARK_HIP(hipGetLastError());
+  }
+  ark::opt_units_set_fresh(opt, true);
   return ARK_OPT_OK;
 }
 
@@ -741,6 +870,40 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
     return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", L.bytes);
   }
   return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws.p, L, s);
+}
+
+int ark_grad_embed_scatter_final(float* embed_grad, uint32_t vocab, uint32_t d,
+                                 const uint32_t* tokens, const float* dx0, uint32_t batch_seq,
+                                 ark_opt_handle* opt) {
+  ark::OptUnits U;
+  uint64_t unit0 = 0;
+  uint32_t seg_flags = 0;
+  int rc = ark::opt_units_for_tensor(opt, embed_grad, (uint64_t)vocab * d, &U, &unit0, &seg_flags);
+  if (rc) return rc;
+  bool skip = false;
+  if ((rc = scatter_check(embed_grad, vocab, d, tokens, dx0, batch_seq, &skip))) return rc;
+  if (skip) return ARK_OPT_OK;  // nothing changes; the units stay valid
+  ark::DeviceGuard g(U.device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", U.device);
+  const ScatterLayout L = scatter_layout(batch_seq, d);
+  StreamBuf ws;
+  hipError_t e = ws.alloc(L.bytes, U.stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the scatter failed", L.bytes);
+  }
+  // the units of the rows it changes are stale from here until rewritten
+  ark::opt_units_set_fresh(opt, false);
+  rc = scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws.p, L, U.stream);
+  if (rc) return rc;
+  if (d % (uint32_t)kTileCols != 0) return ARK_OPT_OK;  // units straddle rows: the step re-reads
+  const uint32_t vec = ((d % 4u) == 0 && (((uintptr_t)embed_grad & 15u) == 0)) ? 1u : 0u;
+  hipLaunchKernelGGL(units_rows_kernel, dim3(batch_seq, d / kTileCols), dim3(kWave), 0, U.stream,
+                     embed_grad, d, (const uint32_t*)((char*)ws.p + L.skeys), vec, U.state,
+                     seg_flags, U.units + unit0);
+  ARK_HIP(hipGetLastError());
+  ark::opt_units_set_fresh(opt, true);
+  return ARK_OPT_OK;
 }
 
 int ark_grad_embed_scatter_noalloc(float* embed_grad, uint32_t vocab, uint32_t d,

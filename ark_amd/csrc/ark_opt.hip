@@ -14,6 +14,7 @@
 #include "ark_codec.h"
 #include "ark_common.hpp"
 #include "ark_grad.h"
+#include "ark_opt_internal.hpp"
 #include "ark_opt_kernels.hpp"
 
 using ark::SegDesc;
@@ -70,6 +71,18 @@ struct ark_opt_handle {
   ark_opt_step_info* d_info = nullptr;
   ark_opt_step_info* h_info = nullptr;  // pinned
   ark_opt_state* h_state = nullptr;     // pinned
+  // the norm's units (fp32-gradient handles): written by the gradient
+  // producers' final kernels, consumed by the next step instead of the read
+  // of every gradient
+  double* d_units = nullptr;
+  bool units_fresh = false;
+  struct TensorInfo {
+    const void* g;
+    uint64_t n;
+    uint64_t seg0;  // index of its first segment
+    uint32_t flags;
+  };
+  std::vector<TensorInfo> tensors;
   // timing
   bool timing = false;
   std::vector<hipEvent_t> ev;  // 4 per pending step
@@ -278,6 +291,9 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   off = align_up(off + sizeof(StepScalars), 256);
   const size_t o_info = off;
   off = align_up(off + sizeof(ark_opt_step_info), 256);
+  const size_t o_units = off;
+  if (hp->grad_dtype == ARK_OPT_GRAD_F32)
+    off = align_up(off + sizeof(double) * (size_t)nseg * ark::kUnitsPerSeg, 256);
 
   hipError_t e = hipMalloc(&h->dev_mem, off);
   if (e != hipSuccess) {
@@ -295,6 +311,16 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->d_state = (ark_opt_state*)(base + o_state);
   h->d_scal = (StepScalars*)(base + o_scal);
   h->d_info = (ark_opt_step_info*)(base + o_info);
+  if (hp->grad_dtype == ARK_OPT_GRAD_F32 && nseg) h->d_units = (double*)(base + o_units);
+  {
+    uint64_t seg0 = 0;
+    h->tensors.reserve((size_t)n_tensors);
+    for (int32_t i = 0; i < n_tensors; ++i) {
+      const ark_opt_tensor& t = tensors[i];
+      h->tensors.push_back({t.g, t.n, seg0, t.flags});
+      seg0 += (t.n + ark::kSeg - 1) / ark::kSeg;
+    }
+  }
   if (hipHostMalloc((void**)&h->h_info, sizeof(ark_opt_step_info), hipHostMallocDefault) != hipSuccess ||
       hipHostMalloc((void**)&h->h_state, sizeof(ark_opt_state), hipHostMallocDefault) != hipSuccess) {
     free_handle(h);
@@ -352,9 +378,16 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
     ARK_HIP(hipEventRecord(ev[0], h->stream));
   }
   if (h->nseg) {
-    ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
-                              h->nseg, h->d_block_fast, h->d_state, h->d_part_sum,
-                              h->nt_from, h->stream));
+    if (h->units_fresh) {
+      // the gradients' producers already formed the tree's first level
+      h->units_fresh = false;
+      ARK_HIP(ark::launch_units_reduce(h->spb, h->norm_blocks, h->d_units, h->d_segs, h->nseg,
+                                       h->d_part_sum, h->stream));
+    } else {
+      ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
+                                h->nseg, h->d_block_fast, h->d_state, h->d_part_sum,
+                                h->nt_from, h->stream));
+    }
     if (h->d_fold)
       ARK_HIP(ark::launch_fold(h->padded_parts, h->d_part_sum, h->d_fold, h->stream));
   }
@@ -378,6 +411,7 @@ int ark_opt_record_overflow(ark_opt_handle* h, ark_opt_step_info* info) {
   if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
   DeviceGuard g(h->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
+  h->units_fresh = false;  // the loss scale they were unscaled by changes
   ARK_HIP(ark::launch_record_overflow(h->hp, h->d_state, h->d_info, h->stream));
   if (info) return finish_info(h, info);
   return ARK_OPT_OK;
@@ -401,6 +435,7 @@ int ark_opt_set_state(ark_opt_handle* h, const ark_opt_state* st) {
   DeviceGuard g(h->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   ARK_HIP(hipStreamSynchronize(h->stream));
+  h->units_fresh = false;  // the loss scale they were unscaled by may change
   *h->h_state = *st;
   ARK_HIP(hipMemcpyAsync(h->d_state, h->h_state, sizeof(ark_opt_state),
                          hipMemcpyHostToDevice, h->stream));
@@ -468,3 +503,67 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
 }
 
 }  // extern "C"
+
+// ---- the norm's units, for the gradient hand-off (ark_opt_internal.hpp) ----
+
+namespace ark {
+
+namespace {
+void fill_units(ark_opt_handle* h, OptUnits* out) {
+  out->units = h->d_units;
+  out->segs = h->d_segs;
+  out->state = h->d_state;
+  out->stream = h->stream;
+  out->device = h->device;
+  out->nseg = h->nseg;
+}
+}  // namespace
+
+int opt_units_for_spans(ark_opt_handle* h, const float* const* dst, const uint64_t* n,
+                        size_t count, OptUnits* out) {
+  if (!h) return fail(ARK_OPT_EINVAL, "optimizer handle is NULL");
+  if (h->hp.grad_dtype != ARK_OPT_GRAD_F32)
+    return fail(ARK_OPT_EINVAL, "the optimizer handle does not take fp32 gradients");
+  size_t j = 0;
+  for (size_t i = 0; i < h->tensors.size(); ++i) {
+    const ark_opt_handle::TensorInfo& t = h->tensors[i];
+    if (t.n == 0) continue;
+    while (j < count && n[j] == 0) ++j;
+    if (j == count)
+      return fail(ARK_OPT_EINVAL, "the plan ends before tensor %zu of the optimizer table", i);
+    if ((const void*)dst[j] != t.g || n[j] != t.n)
+      return fail(ARK_OPT_EINVAL,
+                  "plan span %zu (%p, %llu elements) is not tensor %zu's gradient (%p, %llu)", j,
+                  (const void*)dst[j], (unsigned long long)n[j], i, t.g,
+                  (unsigned long long)t.n);
+    ++j;
+  }
+  while (j < count && n[j] == 0) ++j;
+  if (j != count)
+    return fail(ARK_OPT_EINVAL, "plan span %zu has no tensor in the optimizer table", j);
+  fill_units(h, out);
+  return ARK_OPT_OK;
+}
+
+int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, OptUnits* out,
+                         uint64_t* unit0, uint32_t* seg_flags) {
+  if (!h) return fail(ARK_OPT_EINVAL, "optimizer handle is NULL");
+  if (!h->units_fresh)
+    return fail(ARK_OPT_EINVAL,
+                "the optimizer handle has no gradient units for its next step (run the plan's "
+                "final accumulation first)");
+  for (const ark_opt_handle::TensorInfo& t : h->tensors) {
+    if (t.g == g && t.n == n) {
+      fill_units(h, out);
+      *unit0 = t.seg0 * (uint64_t)kUnitsPerSeg;
+      *seg_flags = (t.flags & ARK_OPT_TENSOR_NO_UNSCALE) ? kSegNoUnscale : 0u;
+      return ARK_OPT_OK;
+    }
+  }
+  return fail(ARK_OPT_EINVAL, "no tensor of the optimizer table has gradient %p of %llu elements",
+              g, (unsigned long long)n);
+}
+
+void opt_units_set_fresh(ark_opt_handle* h, bool fresh) { h->units_fresh = fresh; }
+
+}  // namespace ark

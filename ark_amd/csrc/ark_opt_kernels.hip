@@ -17,6 +17,7 @@
 // faster AdamW on EKO-237M, within one step, so real training sees it too),
 // and streams the rest with non-temporal loads (13 % faster reads).
 #include "ark_device.hpp"
+#include "ark_opt_internal.hpp"
 #include "ark_opt_kernels.hpp"
 
 namespace ark {
@@ -286,6 +287,49 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
       for (int i = 0; i < w; ++i) bsum[i] = bsum[2 * i] + bsum[2 * i + 1];
     part_sum[blk] = any_bad ? __builtin_nan("") : bsum[0];
   }
+}
+
+// ---- kernel 1 from units (ark_opt_internal.hpp) ----------------------------
+
+// One wave per norm block: the block's SPB * kUnitsPerSeg units, zero past a
+// segment's end and past the last segment, summed as a pairwise tree in index
+// order (K consecutive units per lane, then the lanes in lane order).  That is
+// the perfect binary tree sumsq_kernel forms over the block's elements, so
+// the partial has the same bits; a NaN unit (a non-finite gradient) makes the
+// partial NaN.
+template <int SPB>
+__global__ __launch_bounds__(64) void units_reduce_kernel(const double* __restrict__ units,
+                                                          const SegDesc* __restrict__ segs,
+                                                          uint32_t nseg,
+                                                          double* __restrict__ part_sum) {
+  constexpr int U = SPB * kUnitsPerSeg;     // 16 .. 1024 units per block
+  constexpr int K = U >= 64 ? U / 64 : 1;   // units per lane
+  constexpr int L = U >= 64 ? 64 : U;       // lanes holding units
+  static_assert(K <= kUnitsPerSeg, "a lane's units lie in one segment");
+  const uint32_t lane = threadIdx.x;
+  double x = 0.0;
+  if (lane < (uint32_t)L) {
+    const uint32_t u0 = lane * K;
+    const uint32_t s = blockIdx.x * SPB + u0 / kUnitsPerSeg;
+    double q[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) q[k] = 0.0;
+    if (s < nseg) {
+      const uint32_t n = segs[s].n;
+      const double* p = units + (uint64_t)s * kUnitsPerSeg + u0 % kUnitsPerSeg;
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if ((u0 % kUnitsPerSeg + k) * (uint32_t)kUnit < n) q[k] = p[k];
+    }
+#pragma unroll
+    for (int w = K / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int i = 0; i < w; ++i) q[i] = q[2 * i] + q[2 * i + 1];
+    x = q[0];
+  }
+#pragma unroll
+  for (int st = 0; st < log2i(L); ++st) x = x + __shfl_xor(x, 1 << st);
+  if (lane == 0) part_sum[blockIdx.x] = x;
 }
 
 // ---- kernel 2: finalize ----------------------------------------------------
@@ -585,6 +629,27 @@ hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
     default: return hipErrorInvalidValue;
   }
 #undef ARK_SUMSQ
+  return hipGetLastError();
+}
+
+hipError_t launch_units_reduce(int spb, uint32_t nblocks, const double* units,
+                               const SegDesc* segs, uint32_t nseg, double* part_sum,
+                               hipStream_t stream) {
+  const dim3 grid(nblocks), block(64);
+#define ARK_UNITS(SPB)                                                                     \
+  hipLaunchKernelGGL((units_reduce_kernel<SPB>), grid, block, 0, stream, units, segs, nseg, \
+                     part_sum)
+  switch (spb) {
+    case 1: ARK_UNITS(1); break;
+    case 2: ARK_UNITS(2); break;
+    case 4: ARK_UNITS(4); break;
+    case 8: ARK_UNITS(8); break;
+    case 16: ARK_UNITS(16); break;
+    case 32: ARK_UNITS(32); break;
+    case 64: ARK_UNITS(64); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef ARK_UNITS
   return hipGetLastError();
 }
 

@@ -43,8 +43,15 @@ class GradPlan:
                                          C.byref(h)))
         self._h = h
 
-    def run(self):
-        check(lib().ark_grad_plan_run(self._h))
+    def run(self, final_for=None):
+        """dst += src for every pair.  final_for: an Optimizer (fp32
+        gradients) whose next step this is the last accumulation for; the
+        launch also writes that step's norm units, so the step does not
+        read the gradients again."""
+        if final_for is None:
+            check(lib().ark_grad_plan_run(self._h))
+        else:
+            check(lib().ark_grad_plan_run_final(self._h, final_for.handle))
 
     def close(self):
         if self._h:
@@ -58,15 +65,21 @@ class GradPlan:
             pass
 
 
-def embed_scatter(embed_grad, tokens, dx0, noalloc=False):
+def embed_scatter(embed_grad, tokens, dx0, noalloc=False, final_for=None):
     """embed_grad (vocab x d float32) += rows of dx0 (batch x d float32) at
     the rows of tokens (int32/uint32, batch); tokens >= vocab go to row 0.
     noalloc: use the entry point whose workspace is the library's static
-    device array instead of the stream-ordered pool."""
+    device array instead of the stream-ordered pool.  final_for: the
+    Optimizer whose GradPlan.run(final_for=...) came just before; the scatter
+    runs on its stream and keeps its norm units current."""
     _f32(embed_grad), _f32(dx0)
     assert tokens.is_cuda and tokens.is_contiguous() and tokens.element_size() == 4
     vocab, d = embed_grad.shape
     assert dx0.shape == (tokens.numel(), d)
+    args = (embed_grad.data_ptr(), vocab, d, tokens.data_ptr(), dx0.data_ptr(), tokens.numel())
+    if final_for is not None:
+        assert not noalloc
+        check(lib().ark_grad_embed_scatter_final(*args, final_for.handle))
+        return
     fn = lib().ark_grad_embed_scatter_noalloc if noalloc else lib().ark_grad_embed_scatter
-    check(fn(embed_grad.data_ptr(), vocab, d, tokens.data_ptr(), dx0.data_ptr(), tokens.numel(),
-             _stream()))
+    check(fn(*args, _stream()))

@@ -158,6 +158,11 @@ class Optimizer:
                                    C.c_void_p(stream.cuda_stream), C.byref(h)))
         self._h = h
 
+    @property
+    def handle(self):
+        """The ark_opt_handle* (for the gradient hand-off's final calls)."""
+        return self._h
+
     # -- lifecycle ----------------------------------------------------------
     def close(self):
         if self._h:

@@ -21,6 +21,8 @@
 
 #include <stdint.h>
 
+#include "ark_opt.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -55,6 +57,43 @@ int ark_grad_plan_destroy(ark_grad_plan *plan);
 int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
                            const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                            void *stream);
+
+/* The step's norm without its read of the gradients.  The gradient an
+ * optimizer step on fp32 gradients needs is produced here, so the kernels
+ * that write its final values can also form the first level of the norm's
+ * tree: one f64 per 256 consecutive elements of each ARK_OPT_NORM_SEGMENT
+ * segment, the pairwise sum of the squared unscaled gradients (an aligned
+ * subtree of the canonical tree of include/ark_opt.h, so the sum keeps its
+ * bits).  The next ark_opt_step on that handle then reads these (8 B per 256
+ * elements) instead of every gradient (4 B per element).  In the order of
+ * bridge.m:907-948:
+ *   ark_grad_plan_run_final(plan, opt);              every grad += output
+ *   ark_grad_embed_scatter_final(..., opt);          the token scatter
+ *   ark_opt_step(opt, lr, info);
+ * Between the final calls and the step the gradients must not change by
+ * any other route (another accumulation, ark_grad_embed_scatter, a copy): the
+ * step would use the units of the old values.  ark_opt_set_state and
+ * ark_opt_record_overflow discard the units (the loss scale changes), as does
+ * every ark_opt_step after using them; a step without fresh units reads the
+ * gradients as usual. */
+
+/* As ark_grad_plan_run, as the last accumulation before opt's next step:
+ * also writes the norm's units of every span into opt.  opt must take fp32
+ * gradients (ARK_OPT_GRAD_F32), the plan's spans with n > 0 must be, in
+ * order, exactly the gradients of opt's tensors with n > 0, and the plan and
+ * opt must share a stream; ARK_OPT_EINVAL otherwise, before anything is
+ * queued. */
+int ark_grad_plan_run_final(ark_grad_plan *plan, ark_opt_handle *opt);
+
+/* As ark_grad_embed_scatter on opt's stream, after ark_grad_plan_run_final
+ * (ARK_OPT_EINVAL otherwise): embed_grad must be the gradient of one of
+ * opt's tensors with vocab * d elements, and the units of the embedding rows
+ * the scatter changes are rewritten from their final values.  When d is not
+ * a multiple of 256 the units cannot follow rows; the scatter is done and
+ * the next step reads the gradients instead. */
+int ark_grad_embed_scatter_final(float *embed_grad, uint32_t vocab, uint32_t d,
+                                 const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
+                                 ark_opt_handle *opt);
 
 /* Size of the device array behind ark_grad_embed_scatter_noalloc: 48 MiB
  * per GPU, held from the first call on that GPU until the process ends. */

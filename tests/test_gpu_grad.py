@@ -232,19 +232,21 @@ def test_accumulate_and_plan_eko237m():
     assert torch.equal(x, w)
 
 
-def test_handoff_into_optimizer_step():
+@pytest.mark.parametrize("d_model,fused", [(64, False), (256, True), (64, True)])
+def test_handoff_into_optimizer_step(d_model, fused):
     """The backward tail on the device feeding ark_opt_step (fp32 grads):
     every gradient buffer += its backward output (the LM-head add is the
     embedding's), then the token scatter, then one AMP + clip + AdamW step;
     gradients, step scalars and w/m/v against the oracle's loops and
-    optimizer, bit for bit."""
+    optimizer, bit for bit.  fused: the accumulation and the scatter write
+    the norm's units and the step reads them instead of the gradients."""
     torch = _torch()
     from ark_amd import _abi
     from ark_amd.eko import EkoConfig
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
     from oracle import harness as H
 
-    cfg = EkoConfig(n_layers=2, d_model=64, hidden=96, vocab=500)
+    cfg = EkoConfig(n_layers=2, d_model=d_model, hidden=96, vocab=500)
     specs = cfg.tensors()
     rng = np.random.default_rng(11)
     scale = 1024.0
@@ -260,11 +262,12 @@ def test_handoff_into_optimizer_step():
     # device: grads start at zero (training.rs:248), += outputs, then the scatter
     dev_out = [torch.from_numpy(o).cuda() for o in outs]
     plan = grad.GradPlan([(ps.g(i), dev_out[i]) for i in range(len(specs))])
-    plan.run()
-    grad.embed_scatter(ps.g(e).view(cfg.vocab, cfg.d_model),
-                       torch.from_numpy(tokens.view(np.int32)).cuda(), torch.from_numpy(dx0).cuda())
     acfg = AdamConfig(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
     opt = Optimizer(acfg, ps, AmpConfig(loss_scale_init=scale))
+    plan.run(final_for=opt if fused else None)
+    grad.embed_scatter(ps.g(e).view(cfg.vocab, cfg.d_model),
+                       torch.from_numpy(tokens.view(np.int32)).cuda(), torch.from_numpy(dx0).cuda(),
+                       final_for=opt if fused else None)
     _, gi = opt.step_all(3e-4, info=True)
     # host: the same loops, then the oracle optimizer on the same inputs
     host_g = [np.zeros(s.n, np.float32) for s in specs]

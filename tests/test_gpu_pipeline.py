@@ -18,13 +18,18 @@ from ark_amd.eko import EkoConfig
 pytestmark = pytest.mark.gpu
 
 
-def test_training_steps_through_every_row(tmp_path):
+@pytest.mark.parametrize("d_model,fused", [(64, False), (256, True), (64, True)])
+def test_training_steps_through_every_row(tmp_path, d_model, fused):
+    """fused: the last accumulation and the scatter also write the norm's
+    units (ark_grad_plan_run_final, ark_grad_embed_scatter_final), so the
+    step reads no gradient; at d_model 64 the embedding rows do not align
+    with the units and the step reads the gradients again."""
     import torch
     assert torch.cuda.is_available(), "GPU test run without a GPU"
     from ark_amd import _abi, ckpt, codec, grad
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
 
-    mc = EkoConfig(n_layers=2, d_model=64, hidden=96, vocab=300)
+    mc = EkoConfig(n_layers=2, d_model=d_model, hidden=96, vocab=300)
     specs = mc.tensors()
     e = [s.name for s in specs].index("embed")
     rng = np.random.default_rng(2024)
@@ -57,10 +62,10 @@ def test_training_steps_through_every_row(tmp_path):
         for i in range(len(specs)):
             ps.g(i).zero_()                                        # training.rs:248
             outs_dev[i].copy_(torch.from_numpy(outs[i]))
-        gp.run()                                                   # bridge.m:910-915, :931-947
+        gp.run(final_for=opt if fused else None)                   # bridge.m:910-915, :931-947
         grad.embed_scatter(ps.g(e).view(mc.vocab, mc.d_model),     # bridge.m:922-928
                            torch.from_numpy(tokens.view(np.int32)).cuda(),
-                           torch.from_numpy(dx0).cuda())
+                           torch.from_numpy(dx0).cuda(), final_for=opt if fused else None)
         _, gi = opt.step_all(cfg.lr, info=True)                    # training.rs:289-326
         dq.run()                                                   # training.rs:162-186
         # host

@@ -1,0 +1,214 @@
+"""The step's norm from units written by the gradient producers
+(ark_grad_plan_run_final, ark_grad_embed_scatter_final; include/ark_grad.h)
+against the same step reading the gradients (ark_opt_step's own norm pass):
+the global sum of squares must keep its bits, so every step scalar and every
+w/m/v element of the two paths must be identical.  The oracle's agreement
+with the reading path is what tests/test_gpu_parity.py and
+tests/test_gpu_grad.py establish; here the two device paths are compared on
+the full EKO-237M set, on ragged and unaligned tables, with non-finite
+values entering through either producer, and on misuse."""
+import numpy as np
+import pytest
+
+from ark_amd import _abi, grad
+from ark_amd.eko import EKO_237M, EkoConfig, TensorSpec
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0)
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return torch
+
+
+class _Run:
+    """A ParamSet with fp32 gradients, its optimizer and a gradient plan over
+    backward outputs `outs` (shared between runs)."""
+
+    def __init__(self, specs, outs, scale, no_unscale=()):
+        torch = _torch()
+        from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+        self.ps = ParamSet(specs, weight_decay=0.1, grad_dtype=_abi.GRAD_F32,
+                           no_unscale=no_unscale)
+        g = torch.Generator(device="cuda").manual_seed(5)
+        for i, s in enumerate(specs):
+            self.ps.w(i).copy_((torch.randn(s.n, device="cuda", generator=g) * 0.02).half())
+        self.cfg = AdamConfig(**HP)
+        self.opt = Optimizer(self.cfg, self.ps, AmpConfig(loss_scale_init=scale,
+                                                          loss_scale_max=2.0 ** 24))
+        self.plan = grad.GradPlan([(self.ps.g(i), outs[i]) for i in range(len(specs))])
+
+    def step(self, specs, fused, scatter=None):
+        """Zero the gradients, accumulate, scatter, step; returns the info."""
+        for i in range(len(specs)):
+            self.ps.g(i).zero_()
+        self.plan.run(final_for=self.opt if fused else None)
+        if scatter is not None:
+            e, vocab, d, tokens, dx0 = scatter
+            grad.embed_scatter(self.ps.g(e).view(vocab, d), tokens, dx0,
+                               final_for=self.opt if fused else None)
+        _, info = self.opt.step_all(self.cfg.lr, info=True)
+        return info
+
+    def close(self):
+        self.plan.close()
+        self.opt.close()
+
+
+def _same(a, b, specs):
+    torch = _torch()
+    for i in range(len(specs)):
+        for f in ("w", "m", "v"):
+            x, y = getattr(a.ps, f)(i), getattr(b.ps, f)(i)
+            assert torch.equal(x.view(torch.int16 if f == "w" else torch.int32),
+                               y.view(torch.int16 if f == "w" else torch.int32)), (i, f)
+
+
+def _info_eq(x, y):
+    """Step scalars equal; floats compared as bits, NaN matching NaN."""
+    def key(i):
+        f = [np.float64(i.grad_sumsq), np.float32(i.grad_norm), np.float32(i.clip_coef)]
+        return (i.applied, i.clipped) + tuple("nan" if np.isnan(v) else v.tobytes() for v in f)
+    assert key(x) == key(y), (key(x), key(y))
+    assert x.state.as_dict() == y.state.as_dict()
+
+
+def _outs(specs, seed, sigma, scale):
+    torch = _torch()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return [torch.randn(s.n, device="cuda", generator=g) * (sigma * scale) for s in specs]
+
+
+def test_eko237m_units_step_matches_the_reading_step():
+    """All 272 EKO-237M tensors (d 768: the scatter's rows are whole units),
+    a 2 x 2048-token Zipf scatter, gamma_final kept scaled (the reference's
+    quirk flag): five fresh-gradient steps -- two clipped, one with an inf in
+    a layer's backward output (skipped), one with a NaN entering through dx0
+    (skipped), one unclipped."""
+    torch = _torch()
+    specs = EKO_237M.tensors()
+    names = [s.name for s in specs]
+    e = names.index("embed")
+    scale = 65536.0
+    outs = _outs(specs, 11, 1e-4, scale)
+    runs = [_Run(specs, outs, scale, no_unscale=("gamma_final",)) for _ in range(2)]
+    rng = np.random.default_rng(3)
+    vocab, d, n = 32000, 768, 4096
+    for k, (sig, bad_out, bad_dx) in enumerate([(1e-4, False, False), (1e-2, False, False),
+                                                (1e-4, True, False), (1e-4, False, True),
+                                                (3e-5, False, False)]):
+        for o in outs:
+            o.normal_(0.0, sig * scale)
+        if bad_out:
+            outs[names.index("l7.w2")][12345] = float("inf")
+        tokens = torch.from_numpy(((rng.zipf(1.2, n) - 1) % vocab).astype(np.int32)).cuda()
+        dx0 = torch.randn(n, d, device="cuda") * (sig * scale)
+        if bad_dx:
+            dx0[100, 5] = float("nan")
+        infos = [r.step(specs, fused, (e, vocab, d, tokens, dx0))
+                 for r, fused in zip(runs, (False, True))]
+        _info_eq(infos[0], infos[1])
+        assert infos[0].applied == (0 if (bad_out or bad_dx) else 1), k
+        _same(runs[0], runs[1], specs)
+    assert infos[0].state.t == 3
+    for r in runs:
+        r.close()
+
+
+def test_ragged_unaligned_tables_and_small_norm_blocks():
+    """Tensors of 1, 255, 256, 257, 4095, 4097 and 9000 elements (units
+    partly and wholly past a segment's end), a backward output that is only
+    4-byte aligned (the scalar path), a no-unscale tensor, and tables small
+    enough that the norm blocks hold 1, 2 or 4 segments."""
+    torch = _torch()
+    for sizes in ([1, 255, 256, 257, 4095, 4097, 9000], [5000] * 3, [4096] * 40, [300] * 200):
+        specs = [TensorSpec(f"t{i}", (n,), True, False) for i, n in enumerate(sizes)]
+        outs = _outs(specs, len(sizes), 1e-3, 1024.0)
+        base = torch.randn(sizes[0] + 1, device="cuda")
+        outs[0] = base[1:]  # 4-byte aligned only
+        runs = [_Run(specs, outs, 1024.0, no_unscale=(specs[-1].name,)) for _ in range(2)]
+        for k in range(3):
+            infos = [r.step(specs, fused) for r, fused in zip(runs, (False, True))]
+            _info_eq(infos[0], infos[1])
+            _same(runs[0], runs[1], specs)
+            for o in outs:
+                o.mul_(1.5)
+        for r in runs:
+            r.close()
+
+
+def test_units_are_discarded_when_the_loss_scale_or_gradients_change():
+    """After the final accumulation: ark_opt_set_state and
+    ark_opt_record_overflow discard the units (the loss scale they were
+    unscaled by changes), so the next step reads the gradients, here
+    deliberately changed after the units were written; and a step consumes
+    the units, so the one after reads again."""
+    torch = _torch()
+    specs = EkoConfig(n_layers=1, d_model=256, hidden=512, vocab=100).tensors()
+    outs = _outs(specs, 2, 1e-3, 1024.0)
+    a, b = (_Run(specs, outs, 1024.0) for _ in range(2))
+    for r in (a, b):
+        for i in range(len(specs)):
+            r.ps.g(i).zero_()
+    a.plan.run(final_for=a.opt)
+    b.plan.run()
+    for r in (a, b):
+        r.ps.g(0).mul_(3.0)  # changed behind the units' back
+    a.opt.set_state()  # the state as it is
+    ia = a.opt.step_all(a.cfg.lr, info=True)[1]
+    ib = b.opt.step_all(b.cfg.lr, info=True)[1]
+    _info_eq(ia, ib)
+    _same(a, b, specs)
+    for r in (a, b):
+        for i in range(len(specs)):
+            r.ps.g(i).zero_()
+    a.plan.run(final_for=a.opt)
+    b.plan.run()
+    a.opt.record_overflow()
+    b.opt.record_overflow()
+    for r in (a, b):
+        r.ps.g(1).add_(1.0)
+    ia = a.opt.step_all(a.cfg.lr, info=True)[1]
+    ib = b.opt.step_all(b.cfg.lr, info=True)[1]
+    _info_eq(ia, ib)
+    _same(a, b, specs)
+    a.close(), b.close()
+
+
+def test_final_calls_refuse_mismatched_handles():
+    torch = _torch()
+    from ark_amd._lib import ArkOptError, lib
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    specs = EkoConfig(n_layers=1, d_model=256, hidden=512, vocab=100).tensors()
+    e = [s.name for s in specs].index("embed")
+    outs = _outs(specs, 4, 1e-3, 1024.0)
+    r = _Run(specs, outs, 1024.0)
+    tokens = torch.zeros(10, dtype=torch.int32, device="cuda")
+    dx0 = torch.ones(10, 256, device="cuda")
+    emb = r.ps.g(e).view(100, 256)
+    # the scatter's final form needs a final accumulation since the last step
+    with pytest.raises(ArkOptError, match="final accumulation"):
+        grad.embed_scatter(emb, tokens, dx0, final_for=r.opt)
+    # a plan over other buffers, or over a subset, is not the handle's table
+    other = grad.GradPlan([(outs[i], outs[i].clone()) for i in range(len(specs))])
+    with pytest.raises(ArkOptError, match="is not tensor 0's gradient"):
+        other.run(final_for=r.opt)
+    part = grad.GradPlan([(r.ps.g(i), outs[i]) for i in range(len(specs) - 1)])
+    with pytest.raises(ArkOptError, match="ends before tensor"):
+        part.run(final_for=r.opt)
+    # an fp16-gradient handle has no units
+    ps16 = ParamSet(specs, weight_decay=0.1)
+    o16 = Optimizer(AdamConfig(**HP), ps16, AmpConfig())
+    with pytest.raises(ArkOptError, match="fp32 gradients"):
+        r.plan.run(final_for=o16)
+    # a gradient that is no tensor of the table
+    r.plan.run(final_for=r.opt)
+    with pytest.raises(ArkOptError, match="no tensor of the optimizer table"):
+        grad.embed_scatter(outs[e].view(100, 256), tokens, dx0, final_for=r.opt)
+    assert lib().ark_grad_plan_run_final(None, r.opt.handle) == _abi.EINVAL
+    assert lib().ark_grad_plan_run_final(r.plan._h, None) == _abi.EINVAL
+    torch.cuda.synchronize()
+    other.close(), part.close(), o16.close(), r.close()
