@@ -72,6 +72,48 @@ __global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst,
         (__attribute__((address_space(1))) u32x4*)(dst + i));
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+#define ARK_G1 __attribute__((address_space(1)))
+
+template <typename T>
+__device__ __forceinline__ T ldnt(const void* p) {
+  return __builtin_nontemporal_load((const ARK_G1 T*)p);
+}
+template <typename T>
+__device__ __forceinline__ void stnt(void* p, T v) {
+  __builtin_nontemporal_store(v, (ARK_G1 T*)p);
+}
+
+// The optimizer's AdamW row without its arithmetic: one wave per 256-element
+// row, lane l on elements [4l, 4l + 4), non-temporal loads of g (fp16, 8 B),
+// w (fp16, 8 B), m and v (fp32, 16 B each), then non-temporal stores of w, m
+// and v -- the same seven streams, 12 bytes read and 10 written per element,
+// in the same instructions.  Between the loads and the stores a chain of
+// `spacing` dependent fp32 fma stands in for the element math; with k0 = 0,
+// k1 = 1, k2 = 0 (kernel arguments, so the chain cannot be dropped) every
+// stored value equals the loaded one.
+__global__ __launch_bounds__(64) void stream_mix_kernel(uint16_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ g,
+                                                        float* __restrict__ m,
+                                                        float* __restrict__ v, uint32_t spacing,
+                                                        float k0, float k1, float k2) {
+  const uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x * 4u;
+  const u32x2 gg = ldnt<u32x2>(g + e);
+  u32x2 ww = ldnt<u32x2>(w + e);
+  f32x4 mm = ldnt<f32x4>(m + e);
+  f32x4 vv = ldnt<f32x4>(v + e);
+  float acc = (float)((gg.x ^ gg.y) & 1u) + mm.x + vv.x + (float)(ww.x & 1u);
+  for (uint32_t i = 0; i < spacing; ++i) acc = __builtin_fmaf(acc, k1, k2);
+  const float z = acc * k0;  // 0 for finite acc
+  ww.x += (uint32_t)z;
+  mm.x += z;
+  vv.x += z;
+  stnt<u32x2>(w + e, ww);
+  stnt<f32x4>(m + e, mm);
+  stnt<f32x4>(v + e, vv);
+}
+
 uint32_t grid_for(uint64_t n) {
   uint64_t b = (n + 255) / 256;
   if (b > 65536) b = 65536;
@@ -114,6 +156,19 @@ int ark_synth_copy(void* dst, const void* src, uint64_t nbytes, void* stream) {
   if (blocks > 0xFFFFFFFFull / 256u) return -1;
   hipLaunchKernelGGL(copy_kernel, dim3((uint32_t)blocks), dim3(256), 0,
                      (hipStream_t)stream, (u32x4*)dst, (const u32x4*)src, n);
+  return status(hipGetLastError());
+}
+
+int ark_synth_stream_mix(uint16_t* w, const uint16_t* g, float* m, float* v, uint64_t n,
+                         uint32_t spacing, void* stream) {
+  if (n == 0) return 0;
+  if (!w || !g || !m || !v || (n % 256u) ||
+      (((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u))
+    return -1;
+  const uint64_t rows = n / 256u;
+  if (rows > 0x7FFFFFFFull / 64u) return -1;
+  hipLaunchKernelGGL(stream_mix_kernel, dim3((uint32_t)rows), dim3(64), 0, (hipStream_t)stream, w,
+                     g, m, v, spacing, 0.0f, 1.0f, 0.0f);
   return status(hipGetLastError());
 }
 

@@ -41,6 +41,9 @@ def step_bytes(grad):
 WORKLOADS = {
     "c2": dict(desc="EKO-237M: 30 layers, d 768, ffn 2048, tied embed 32000x768 (272 tensors)",
                loss_scale=65536.0, sigma="loguniform"),
+    "c3": dict(desc="EKO-237M AMP stress set (272 tensors): applied steps, then skipped steps "
+                    "(an inf in one gradient; training.rs:293-305)",
+               loss_scale=65536.0, sigma="loguniform"),
     "c4": dict(desc="1.3B scale-up: 24 layers, d 2048, ffn 5504, tied embed 32000x2048 (218 tensors)",
                loss_scale=65536.0, sigma=1e-3),
     "c1": dict(desc="one EKO layer (9 tensors)", loss_scale=1024.0, sigma=1e-3),
@@ -82,7 +85,9 @@ def _run_gpu(name, steps, warmup, stream, grad="f16"):
     w = WORKLOADS[name]
     sig = sigmas_for(name, specs)
     cfg = AdamConfig(**HP)
-    amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24)
+    # c3 times skipped steps back to back: no early stop after 200 of them
+    amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24,
+                    max_consecutive_nonfinite=(2 ** 31 if name == "c3" else 200))
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
     gdt = _abi.GRAD_F16 if grad == "f16" else _abi.GRAD_F32
     ps = synth.problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"], grad_dtype=gdt)
@@ -128,8 +133,9 @@ def _run_gpu(name, steps, warmup, stream, grad="f16"):
     del graph
 
     _, last = opt.step_all(cfg.lr, info=True)
+    skip = _time_skipped(ps, opt, cfg, steps) if name == "c3" else None
     n = ps.n_params
-    res = dict(
+    res = dict(skip=skip,
         n_params=n, n_tensors=len(specs), ms_step=ms_step,
         ms_adamw=tm.ms_adamw / tm.steps, ms_norm=tm.ms_norm / tm.steps,
         ms_finalize=tm.ms_finalize / tm.steps, ms_step_events=tm.ms_step / tm.steps,
@@ -140,6 +146,42 @@ def _run_gpu(name, steps, warmup, stream, grad="f16"):
     del ps
     torch.cuda.empty_cache()
     return res
+
+
+def _time_skipped(ps, opt, cfg, steps):
+    """steps skipped steps (training.rs:293-305): +inf planted in one fp16
+    gradient, so the norm pass flags it, the finalize halves the loss scale
+    and counts the skip, and the AdamW pass exits at once.  Wall clock over
+    the steps, and the kernels with the handle's events; the gradient is
+    restored afterwards."""
+    import torch
+    g16 = ps.g(0).view(torch.int16)
+    old = int(g16[0].item())
+    g16[0] = 0x7C00  # +inf
+    _, first = opt.step_all(cfg.lr, info=True)
+    assert first.applied == 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step_all(cfg.lr)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    opt.set_timing(True)
+    for _ in range(steps):
+        opt.step_all(cfg.lr)
+    torch.cuda.synchronize()
+    tm = opt.get_timing()
+    opt.set_timing(False)
+    _, last = opt.step_all(cfg.lr, info=True)
+    g16[0] = old
+    assert last.applied == 0 and last.state.skipped_steps >= 2 * steps + 2
+    log(f"[bench] skipped step: {wall_ms:.4f} ms (norm {tm.ms_norm / tm.steps:.4f}, finalize "
+        f"{tm.ms_finalize / tm.steps:.4f}, adamw exit {tm.ms_adamw / tm.steps:.4f})")
+    return dict(ms_per_skipped_step=round(wall_ms, 4),
+                kernels_ms={"sumsq": round(tm.ms_norm / tm.steps, 4),
+                            "finalize": round(tm.ms_finalize / tm.steps, 4),
+                            "adamw_exit": round(tm.ms_adamw / tm.steps, 4)},
+                skipped_total=int(last.state.skipped_steps))
 
 
 def _run_fused(specs, ps, opt, cfg, steps, warmup, stream):
@@ -225,6 +267,80 @@ def _run_fused(specs, ps, opt, cfg, steps, warmup, stream):
     del ps
     torch.cuda.empty_cache()
     return res
+
+
+def run_ceiling(a):
+    """The measured ceiling of the AdamW pass's access pattern, on the same
+    memory as the pass: the stream-mix probe (ark_synth_stream_mix: AdamW's
+    one-wave-per-row shape, seven streams and cache hints, 22 B/param, its
+    arithmetic replaced by a chain of `spacing` dependent fma) run over the
+    workload's own parameter arenas.  First a spacing sweep (median of
+    --steps launches each, HIP events); then --steps rounds that each time
+    one probe launch at the best spacing and one optimizer step with the
+    handle's per-kernel events, so the probe and the AdamW pass are compared
+    interleaved on the same box and the same pages."""
+    import torch
+    from ark_amd import synth
+    from ark_amd.eko import config_tensors
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    torch.cuda.set_device(0)
+    name = a.workload
+    specs = config_tensors(name)
+    w = WORKLOADS[name]
+    cfg = AdamConfig(**HP)
+    ps = synth.problem(specs, SEED, cfg.weight_decay, sigmas_for(name, specs), w["loss_scale"])
+    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24))
+    n = ps.total - ps.total % 256
+    arenas = (ps.w_arena[:n].view(torch.int16), ps.g_arena[:n].view(torch.int16),
+              ps.m_arena[:n], ps.v_arena[:n])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def probe(spacing):
+        e0.record()
+        synth.stream_mix(*arenas, spacing)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    sweep = []
+    for spacing in (0, 16, 32, 64, 128, 256):
+        probe(spacing)
+        ms = sorted(probe(spacing) for _ in range(a.steps))[a.steps // 2]
+        sweep.append(dict(spacing=spacing, ms=round(ms, 4),
+                          gbs=round(22 * n / (ms * 1e-3) / 1e9, 1)))
+        log(f"[bench] stream mix spacing {spacing:4d}: {ms:.4f} ms = {sweep[-1]['gbs']} GB/s")
+    best = min(sweep, key=lambda r: r["ms"])["spacing"]
+    for _ in range(3):
+        opt.step_all(cfg.lr)
+    probe_ms, adam_ms = [], []
+    for _ in range(a.steps):
+        probe_ms.append(probe(best))
+        opt.set_timing(True)
+        opt.step_all(cfg.lr)
+        torch.cuda.synchronize()
+        tm = opt.get_timing()
+        opt.set_timing(False)
+        adam_ms.append(tm.ms_adamw / tm.steps)
+    pm = sorted(probe_ms)[a.steps // 2]
+    am = sorted(adam_ms)[a.steps // 2]
+    n_params = ps.n_params
+    log(f"[bench] interleaved: probe {pm:.4f} ms ({n} elements), AdamW {am:.4f} ms "
+        f"({n_params} params): AdamW / probe per element {am / pm * n / n_params:.4f}")
+    out = {
+        "metric": "AdamW stream-mix ceiling (22 B/param, 1 GPU) GB/s",
+        "value": round(22 * n / (pm * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": 1, "ms_per_step": round(pm, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u16/f32 copy", "data": "synthetic",
+        "config": {"workload": f"{name}: the optimizer's parameter arenas ({n} elements; "
+                               f"{n_params} params)",
+                   "sweep": sweep, "best_spacing": best,
+                   "interleaved": {"probe_ms": round(pm, 4), "adamw_ms": round(am, 4),
+                                   "adamw_gbs": round(22 * n_params / (am * 1e-3) / 1e9, 1),
+                                   "adamw_over_probe_per_element":
+                                       round(am / pm * n / n_params, 4)}},
+    }
+    opt.close()
+    print(json.dumps(out), flush=True)
 
 
 def calib_copy(nbytes=1 << 30, reps=3):
@@ -645,10 +761,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", default="step", choices=["step", "codec", "ckpt", "grad", "dropin"],
+    ap.add_argument("--path", default="step",
+                    choices=["step", "codec", "ckpt", "grad", "dropin", "ceiling"],
                     help="step: the optimizer step (headline); codec: the weight codec; "
                          "ckpt: the V4 checkpoint image; grad: the gradient hand-off; "
-                         "dropin: the reference's 272 single-tensor calls per step")
+                         "dropin: the reference's 272 single-tensor calls per step; "
+                         "ceiling: the AdamW pass's access pattern without its arithmetic")
     ap.add_argument("--grad", default="f16", choices=["f16", "f32", "f32-fused"],
                     help="step: gradient type handed to the step (f16 loss-scaled, as the benchmark "
                          "configurations; f32, as the gradient hand-off produces; f32-fused, "
@@ -662,7 +780,8 @@ def main():
               "single MI355X (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if a.path != "step":
-        {"codec": run_codec, "ckpt": run_ckpt, "grad": run_grad, "dropin": run_dropin}[a.path](a)
+        {"codec": run_codec, "ckpt": run_ckpt, "grad": run_grad, "dropin": run_dropin,
+         "ceiling": run_ceiling}[a.path](a)
         if a.calib_copy:
             calib_copy()
         return
@@ -723,6 +842,12 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if r.get("skip"):
+        out["config"]["skipped_steps"] = dict(
+            r["skip"], ms_per_applied_step=round(r["ms_step"], 4),
+            bytes_per_skipped_step=2 * n,
+            note="an inf in one gradient: the norm pass reads g (2 B/param) and flags it, the "
+            "finalize skips, the AdamW pass exits before any access")
     if a.grad == "f32-fused":
         out["config"]["fused_norm"] = dict(
             r["fused"], note="ms_per_step: the step after the gradient plan's final "

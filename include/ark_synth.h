@@ -51,6 +51,16 @@ int ark_synth_fill_u16(uint16_t *out, uint64_t n, uint16_t bits, void *stream);
  * WRITE_SIZE) in profiles. */
 int ark_synth_copy(void *dst, const void *src, uint64_t nbytes, void *stream);
 
+/* The optimizer's AdamW pass without its arithmetic: one wave per
+ * 256-element row reads g (fp16), w (fp16), m and v (fp32) and writes w, m
+ * and v back unchanged, with the same instructions and cache hints, and a
+ * chain of `spacing` dependent fp32 fma between the loads and the stores in
+ * place of the element math.  22 bytes per element, the pass's stream mix:
+ * the measured ceiling for that access pattern.  n a multiple of 256, every
+ * pointer 16-byte aligned; returns -1 otherwise. */
+int ark_synth_stream_mix(uint16_t *w, const uint16_t *g, float *m, float *v, uint64_t n,
+                         uint32_t spacing, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
