@@ -10,7 +10,9 @@ import os
 from . import _abi
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libark_opt.so")
+# ARK_OPT_LIB names another build of the same library (the sanitizer build
+# the CPU tests load); by default the in-tree one.
+LIB_PATH = os.environ.get("ARK_OPT_LIB") or os.path.join(_HERE, "lib", "libark_opt.so")
 CSRC = os.path.join(_HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
 
