@@ -162,11 +162,35 @@ def save_params(path, params, opt, global_step):
     save(path, param_tensors(params), global_step, st.t, st)
 
 
+def file_tensors(params, version, n_tensors):
+    """The ParamSet buffers a file of this version and tensor count fills, in
+    file order, as the reference reads them:
+    * V4 / V3: param_tensors(params), without gamma_final's w, m, v when the
+      file has 3 + 27 L tensors (io.rs:560-565 tells the two apart by the
+      count; V3 never has it, io.rs:614-616), which then stay as they are;
+    * V2: the weights only, embed and each layer's 9 (the 1 + 9 L tensors
+      training.rs:488-509 accepts)."""
+    has_gf = any(s.name == "gamma_final" for s in params.specs)
+    if version == 2:
+        return param_tensors(params, with_moments=False)
+    full = param_tensors(params)
+    if has_gf and n_tensors == len(full) - 3:
+        return full[:-3]
+    return full
+
+
 def load_params(path, params, opt=None):
-    """Resume: fill the ParamSet from the file; with opt, set its t to the
-    file's adam_step (optimizer.rs:308) and restore the loss-scaler state
-    when the file carries it."""
-    info, amp = load(path, param_tensors(params))
+    """Resume: fill the ParamSet from the file (the tensors file_tensors
+    names; the library refuses a file whose count or sizes differ).  With
+    opt, set its t to the file's adam_step (optimizer.rs:308) and restore
+    the loss-scaler state when the file carries it.  A V2 file holds weights
+    only: the reference starts the optimizer from zero after it
+    (training.rs:488-509), so the moments are zeroed and t set to 0."""
+    head, _ = probe(path)
+    info, amp = load(path, file_tensors(params, head.version, head.n_tensors))
+    if info.version == 2:
+        params.m_arena.zero_()
+        params.v_arena.zero_()
     if opt is not None:
         if amp is not None:
             opt.set_state(**{k: getattr(amp, k) for k, _ in _abi.State._fields_

@@ -27,11 +27,14 @@
 // overlapped, each chunk's file I/O split over several threads.
 #include <errno.h>
 #include <fcntl.h>
+#include <limits.h>
+#include <stdlib.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <string>
 #include <thread>
 #include <vector>
@@ -592,6 +595,23 @@ void sync_parent_dir(const char* path) {
   (void)::close(d);
 }
 
+std::atomic<uint64_t> g_tmp_counter{0};
+
+// The file a save to path replaces: path itself, or the file a symbolic
+// link at path resolves to.
+std::string save_target(const char* path) {
+  struct stat st;
+  if (lstat(path, &st) == 0 && S_ISLNK(st.st_mode)) {
+    char* r = realpath(path, nullptr);
+    if (r) {
+      std::string t(r);
+      free(r);
+      return t;
+    }
+  }
+  return std::string(path);
+}
+
 int read_exact(int fd, void* buf, uint64_t len, uint64_t off, const char* path) {
   uint8_t* p = (uint8_t*)buf;
   while (len) {
@@ -873,12 +893,23 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
     }
   } eg{ev};
   StreamSync sync{s};
-  // Written to <path>.tmp and renamed over path once complete: a save that
-  // fails leaves no partial file (one that fallocate has sized in full would
-  // pass a loader's length checks) and any earlier checkpoint at path intact.
-  const std::string tmp = std::string(path) + ".tmp";
+  // Written to a temporary file beside the target and renamed over it once
+  // complete: a save that fails leaves no partial file (one that fallocate
+  // has sized in full would pass a loader's length checks) and any earlier
+  // checkpoint intact.  The temporary name is unique to this call
+  // (<target>.tmp.<pid>.<n>, created with O_EXCL), so concurrent saves and a
+  // user's own files never share it.  A symbolic link at path is followed, as
+  // File::create follows it (io.rs:450): the link stays and its target
+  // becomes the new file (a dangling link is replaced by the file).
+  const std::string target = save_target(path);
+  std::string tmp;
   Fd f;
-  f.fd = ::open(tmp.c_str(), O_RDWR | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+  for (int attempt = 0; attempt < 16 && f.fd < 0; ++attempt) {
+    tmp = target + ".tmp." + std::to_string((long)getpid()) + "." +
+          std::to_string(g_tmp_counter.fetch_add(1));
+    f.fd = ::open(tmp.c_str(), O_RDWR | O_CREAT | O_EXCL | O_CLOEXEC, 0644);
+    if (f.fd < 0 && errno != EEXIST) break;
+  }
   if (f.fd < 0) return io_fail("create", tmp.c_str());
   struct TmpFile {
     const std::string& name;
@@ -930,9 +961,9 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
   const int fd = f.fd;
   f.fd = -1;
   if (::close(fd) != 0) return io_fail("close", tmp.c_str());
-  if (::rename(tmp.c_str(), path) != 0) return io_fail("rename to", path);
+  if (::rename(tmp.c_str(), target.c_str()) != 0) return io_fail("rename to", target.c_str());
   tmp_file.done = true;
-  sync_parent_dir(path);
+  sync_parent_dir(target.c_str());
   return ARK_OPT_OK;
 }
 

@@ -80,10 +80,13 @@ typedef struct ark_ckpt_info {
 } ark_ckpt_info;
 
 /* CheckpointV3::save_fp16 (io.rs:432-500): writes the file as
- * "<path>.tmp" and renames it to path once complete, so a failed save
- * leaves no partial file and an existing file at path unchanged.  amp may be
- * NULL (no trailer).  The records are read on the given stream; the call
- * returns when the file is written, closed and renamed. */
+ * "<target>.tmp.<pid>.<n>" (created exclusively, unique to the call) and
+ * renames it over the target once complete, so a failed save leaves no
+ * partial file and an existing file unchanged.  The target is path, or the
+ * file a symbolic link at path resolves to (the link is kept, as File::create
+ * keeps it; io.rs:450).  amp may be NULL (no trailer).  The records are read
+ * on the given stream; the call returns when the file is written, flushed,
+ * closed and renamed. */
 int ark_ckpt_save_v4(const char *path, uint64_t global_step, uint64_t adam_step,
                      const ark_ckpt_record *records, int32_t n_records,
                      const ark_opt_state *amp, void *stream);

@@ -173,7 +173,11 @@ int ark_opt_destroy(ark_opt_handle *h);
  * update of training.rs:289-326 with Optimizer::step_all
  * (optimizer.rs:171-228).  Stream ordered; with info == NULL nothing waits
  * on the host.  `lr` is this step's learning rate (Optimizer::lr_now,
- * optimizer.rs:80-92, evaluated by the caller). */
+ * optimizer.rs:80-92, evaluated by the caller).  It travels as a kernel
+ * argument: a HIP graph that captured a step replays the lr it was captured
+ * with (t, the bias corrections and the AMP state still advance on the
+ * device), so a schedule that changes lr needs a graph per lr value or a
+ * fresh capture. */
 int ark_opt_step(ark_opt_handle *h, float lr, ark_opt_step_info *info);
 
 /* The external skip path of training.rs:228-241: the caller found a

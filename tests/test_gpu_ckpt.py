@@ -370,16 +370,114 @@ def test_entry_points_reject_host_or_short_buffers(tmp_path):
 
 
 def test_save_replaces_the_file_whole(tmp_path):
-    """A save goes through <path>.tmp and a rename: afterwards only the
-    finished file is there, and it replaces an earlier one completely."""
+    """A save goes through a temporary file and a rename: afterwards only the
+    finished file is there (and a user's own ckpt.ark.tmp, untouched), and it
+    replaces an earlier one completely."""
     import os
     import torch
     path = tmp_path / "ckpt.ark"
     path.write_bytes(b"an earlier, longer file " * 1000)
+    (tmp_path / "ckpt.ark.tmp").write_bytes(b"the user's own file")
     w = torch.arange(777, dtype=torch.float32, device="cuda").half()
     m = torch.full((777,), 0.5, device="cuda")
     ckpt.save(str(path), [w, m], 12, 34)
     torch.cuda.synchronize()
-    assert sorted(os.listdir(tmp_path)) == ["ckpt.ark"]
+    assert sorted(os.listdir(tmp_path)) == ["ckpt.ark", "ckpt.ark.tmp"]
+    assert (tmp_path / "ckpt.ark.tmp").read_bytes() == b"the user's own file"
     want = K.write_v4(12, 34, [w.cpu().numpy().view(np.uint16), m.cpu().numpy()])
     assert path.read_bytes() == want
+
+
+def test_failed_save_keeps_the_earlier_state(tmp_path):
+    """Host-side failures after the data is written: when the rename fails
+    (the path is a non-empty directory) the call returns ARK_OPT_EIO, the
+    directory is as it was and no temporary file is left; when the directory
+    cannot be written the temporary file cannot be created (EIO, nothing
+    left either).  A symbolic link at the path is followed: the link stays
+    and its target holds the new checkpoint."""
+    import os
+    import stat
+    import torch
+    from ark_amd._lib import lib
+    L = lib()
+    w = torch.arange(300, dtype=torch.float32, device="cuda").half()
+    recs = (_abi.CkptRecord * 1)()
+    recs[0] = _abi.CkptRecord(w.data_ptr(), 300, _abi.CKPT_F16, 0)
+    want = K.write_v4(5, 6, [w.cpu().numpy().view(np.uint16)])
+    # rename over a non-empty directory fails after the whole file was written
+    d = tmp_path / "ckpt.ark"
+    d.mkdir()
+    (d / "inside").write_bytes(b"keep me")
+    rc = L.ark_ckpt_save_v4(os.fsencode(str(d)), 5, 6, recs, 1, None, None)
+    assert rc == _abi.EIO and "rename" in L.ark_opt_last_error().decode()
+    assert sorted(os.listdir(tmp_path)) == ["ckpt.ark"]
+    assert sorted(os.listdir(d)) == ["inside"] and (d / "inside").read_bytes() == b"keep me"
+    # a directory that cannot be written: no temporary file, the old file kept
+    ro = tmp_path / "ro"
+    ro.mkdir()
+    old = ro / "c.ark"
+    old.write_bytes(b"earlier checkpoint")
+    ro.chmod(stat.S_IRUSR | stat.S_IXUSR)
+    try:
+        if not os.access(ro, os.W_OK):  # root can write anyway
+            rc = L.ark_ckpt_save_v4(os.fsencode(str(old)), 5, 6, recs, 1, None, None)
+            assert rc == _abi.EIO and "create" in L.ark_opt_last_error().decode()
+            assert sorted(os.listdir(ro)) == ["c.ark"] and old.read_bytes() == b"earlier checkpoint"
+    finally:
+        ro.chmod(stat.S_IRWXU)
+    # a symbolic link at the path: the link stays, its target is replaced
+    real = tmp_path / "real.ark"
+    real.write_bytes(b"old")
+    link = tmp_path / "latest.ark"
+    link.symlink_to(real)
+    assert L.ark_ckpt_save_v4(os.fsencode(str(link)), 5, 6, recs, 1, None, None) == 0
+    assert link.is_symlink() and os.readlink(link) == str(real)
+    assert real.read_bytes() == want
+    assert sorted(os.listdir(tmp_path)) == ["ckpt.ark", "latest.ark", "real.ark", "ro"]
+
+
+@pytest.mark.parametrize("kind", ["v4_without_gamma_final", "v2_weights_only"])
+def test_load_params_follows_the_file(tmp_path, kind):
+    """load_params on the files the reference also resumes from: a V4 file
+    without gamma_final fills everything else (gamma_final stays as it was)
+    and sets t; a V2 file fills the weights, zeroes the moments and sets t
+    to 0 (training.rs:488-509)."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    cfg = EkoConfig(n_layers=2, d_model=16, hidden=24, vocab=40)
+    ps = _params(cfg, 4)
+    opt = Optimizer(AdamConfig(), ps, AmpConfig())
+    opt.set_state(t=99)
+    g = [sp.name for sp in ps.specs].index("gamma_final")
+    before = {f: getattr(ps, f)(g).clone() for f in "wmv"}
+    rng = np.random.default_rng(8)
+    path = tmp_path / "f.ark"
+    if kind == "v4_without_gamma_final":
+        tens = ckpt.file_tensors(ps, 4, 3 + 27 * 2)
+        host = [rng.integers(0, 0x7C00, t.numel(), dtype=np.uint32).astype(np.uint16)
+                if t.element_size() == 2 else rng.standard_normal(t.numel()).astype(np.float32)
+                for t in tens]
+        path.write_bytes(K.write_v4(7, 31, host))
+    else:
+        tens = ckpt.file_tensors(ps, 2, 1 + 9 * 2)
+        host = [rng.standard_normal(t.numel()).astype(np.float32) for t in tens]
+        path.write_bytes(K.write_v2(7, host))
+    info, amp = ckpt.load_params(str(path), ps, opt)
+    torch.cuda.synchronize()
+    assert amp is None and info.global_step == 7
+    for t, h in zip(tens, host):
+        got = _bits(t)
+        want = h.view(np.uint16) if t.element_size() == 2 else h.view(np.uint32)
+        if t.element_size() == 2 and h.dtype == np.float32:  # V2 fp32 into fp16 weights
+            want = oracle.f32_to_f16(h).view(np.uint16)
+        np.testing.assert_array_equal(got, want)
+    if kind == "v4_without_gamma_final":
+        assert opt.get_state().t == 31
+        for f in "wmv":
+            assert torch.equal(getattr(ps, f)(g), before[f])
+    else:
+        assert opt.get_state().t == 0
+        assert torch.count_nonzero(ps.m_arena).item() == 0
+        assert torch.count_nonzero(ps.v_arena).item() == 0
+        assert torch.equal(ps.w(g), before["w"])
+    opt.close()

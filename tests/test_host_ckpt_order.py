@@ -64,3 +64,29 @@ def test_oracle_loader_regroups_that_order():
         np.testing.assert_array_equal(a.view(np.uint32),
                                       b.astype(np.uint16).view(np.float16).astype(np.float32)
                                       .view(np.uint32))
+
+
+def test_file_tensors_follow_what_the_file_holds():
+    """load_params reads the tensors the file has: the full V4 order; V4
+    without gamma_final (3 + 27 L tensors, io.rs:560-565) leaves it out; V3
+    (never has it, io.rs:614-616) the same; V2 the weights only, embed and
+    each layer's 9 (training.rs:488-509)."""
+    cfg = EkoConfig(n_layers=2, d_model=8, hidden=12, vocab=10)
+    ps = _cpu_params(cfg)
+    full = _names(ps, ckpt.param_tensors(ps))
+    assert _names(ps, ckpt.file_tensors(ps, 4, 3 + 27 * 2 + 3)) == full
+    no_gf = _names(ps, ckpt.file_tensors(ps, 4, 3 + 27 * 2))
+    assert no_gf == full[:-3] and all(n != "gamma_final" for n, _ in no_gf)
+    assert _names(ps, ckpt.file_tensors(ps, 3, 3 + 27 * 2)) == full[:-3]
+    v2 = _names(ps, ckpt.file_tensors(ps, 2, 1 + 9 * 2))
+    lw = ["wq", "wk", "wv", "wo", "w1", "w2", "w3", "g1", "g2"]
+    assert v2 == [("embed", "w")] + [(f"l{l}.{k}", "w") for l in range(2) for k in lw]
+    # a count that matches neither is passed through whole: the library's
+    # count check then refuses the file
+    assert _names(ps, ckpt.file_tensors(ps, 4, 7)) == full
+    # the oracle's reader regroups a gamma-less V4 file into the same weights
+    rng = np.random.default_rng(3)
+    host = [rng.standard_normal(t.numel()).astype(np.float32)
+            for t in ckpt.file_tensors(ps, 4, 3 + 27 * 2)]
+    r = K.load(K.write_v4(1, 2, host))
+    assert len(r["pesos"]) == 1 + 18 and len(r["momentos_m"]) == 1 + 18
