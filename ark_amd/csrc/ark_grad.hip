@@ -878,7 +878,11 @@ int ark_grad_embed_scatter_final(float* embed_grad, uint32_t vocab, uint32_t d,
   ark::OptUnits U;
   uint64_t unit0 = 0;
   uint32_t seg_flags = 0;
-  int rc = ark::opt_units_for_tensor(opt, embed_grad, (uint64_t)vocab * d, &U, &unit0, &seg_flags);
+  // rows are whole units only when d is a multiple of 256; otherwise the
+  // scatter is done and the step reads the gradients (no units needed here)
+  const bool rows_are_units = d % (uint32_t)kTileCols == 0;
+  int rc = ark::opt_units_for_tensor(opt, embed_grad, (uint64_t)vocab * d, rows_are_units, &U,
+                                     &unit0, &seg_flags);
   if (rc) return rc;
   bool skip = false;
   if ((rc = scatter_check(embed_grad, vocab, d, tokens, dx0, batch_seq, &skip))) return rc;
@@ -896,7 +900,7 @@ int ark_grad_embed_scatter_final(float* embed_grad, uint32_t vocab, uint32_t d,
   ark::opt_units_set_fresh(opt, false);
   rc = scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws.p, L, U.stream);
   if (rc) return rc;
-  if (d % (uint32_t)kTileCols != 0) return ARK_OPT_OK;  // units straddle rows: the step re-reads
+  if (!rows_are_units) return ARK_OPT_OK;  // units straddle rows: the step re-reads
   const uint32_t vec = ((d % 4u) == 0 && (((uintptr_t)embed_grad & 15u) == 0)) ? 1u : 0u;
   hipLaunchKernelGGL(units_rows_kernel, dim3(batch_seq, d / kTileCols), dim3(kWave), 0, U.stream,
                      embed_grad, d, (const uint32_t*)((char*)ws.p + L.skeys), vec, U.state,

@@ -545,10 +545,10 @@ int opt_units_for_spans(ark_opt_handle* h, const float* const* dst, const uint64
   return ARK_OPT_OK;
 }
 
-int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, OptUnits* out,
-                         uint64_t* unit0, uint32_t* seg_flags) {
+int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, bool require_fresh,
+                         OptUnits* out, uint64_t* unit0, uint32_t* seg_flags) {
   if (!h) return fail(ARK_OPT_EINVAL, "optimizer handle is NULL");
-  if (!h->units_fresh)
+  if (require_fresh && !h->units_fresh)
     return fail(ARK_OPT_EINVAL,
                 "the optimizer handle has no gradient units for its next step (run the plan's "
                 "final accumulation first)");

@@ -42,10 +42,10 @@ int opt_units_for_spans(ark_opt_handle* h, const float* const* dst, const uint64
                         size_t count, OptUnits* out);
 
 // The tensor of h whose gradient is g with n elements: *unit0 = the index of
-// its first unit, *seg_flags = its segments' flags.  Fails unless h's units
-// are fresh (written since its last step).
-int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, OptUnits* out,
-                         uint64_t* unit0, uint32_t* seg_flags);
+// its first unit, *seg_flags = its segments' flags.  With require_fresh it
+// fails unless h's units are fresh (written since its last step).
+int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, bool require_fresh,
+                         OptUnits* out, uint64_t* unit0, uint32_t* seg_flags);
 
 // Marks h's units as written for its next step (fresh) or not.
 void opt_units_set_fresh(ark_opt_handle* h, bool fresh);

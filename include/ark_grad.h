@@ -89,8 +89,9 @@ int ark_grad_plan_run_final(ark_grad_plan *plan, ark_opt_handle *opt);
  * (ARK_OPT_EINVAL otherwise): embed_grad must be the gradient of one of
  * opt's tensors with vocab * d elements, and the units of the embedding rows
  * the scatter changes are rewritten from their final values.  When d is not
- * a multiple of 256 the units cannot follow rows; the scatter is done and
- * the next step reads the gradients instead. */
+ * a multiple of 256 the units cannot follow rows: the scatter is done (with
+ * or without a final accumulation before it) and the next step reads the
+ * gradients instead. */
 int ark_grad_embed_scatter_final(float *embed_grad, uint32_t vocab, uint32_t d,
                                  const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                                  ark_opt_handle *opt);

@@ -192,6 +192,17 @@ def test_final_calls_refuse_mismatched_handles():
     # the scatter's final form needs a final accumulation since the last step
     with pytest.raises(ArkOptError, match="final accumulation"):
         grad.embed_scatter(emb, tokens, dx0, final_for=r.opt)
+    # ... unless its rows cannot be units (d % 256 != 0): then it only scatters,
+    # as often as asked, and the step reads the gradients
+    ps5 = ParamSet([TensorSpec("e", (50, 20), True, False)], 0.1, grad_dtype=_abi.GRAD_F32)
+    o5 = Optimizer(AdamConfig(**HP), ps5, AmpConfig())
+    t5 = torch.tensor([1, 3, 1], dtype=torch.int32, device="cuda")
+    x5 = torch.ones(3, 20, device="cuda")
+    for _ in range(2):
+        grad.embed_scatter(ps5.g(0).view(50, 20), t5, x5, final_for=o5)
+    torch.cuda.synchronize()
+    assert ps5.g(0).view(50, 20)[1].tolist() == [4.0] * 20
+    o5.close()
     # a plan over other buffers, or over a subset, is not the handle's table
     other = grad.GradPlan([(outs[i], outs[i].clone()) for i in range(len(specs))])
     with pytest.raises(ArkOptError, match="is not tensor 0's gradient"):
