@@ -38,6 +38,7 @@ def _declare(L):
                             C.POINTER(H)], C.c_int),
         "ark_opt_destroy": ([H], C.c_int),
         "ark_opt_step": ([H, f32, C.POINTER(_abi.StepInfo)], C.c_int),
+        "ark_opt_step_lr_dev": ([H, P, C.POINTER(_abi.StepInfo)], C.c_int),
         "ark_opt_record_overflow": ([H, C.POINTER(_abi.StepInfo)], C.c_int),
         "ark_opt_get_state": ([H, C.POINTER(_abi.State)], C.c_int),
         "ark_opt_set_state": ([H, C.POINTER(_abi.State)], C.c_int),

@@ -363,9 +363,11 @@ static int finish_info(ark_opt_handle* h, ark_opt_step_info* info) {
   return info->status;
 }
 
-int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
-  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
-  if (!finite_f(lr)) return fail(ARK_OPT_EINVAL, "lr must be finite");
+namespace {
+
+// ark_opt_step with lr given on the host (lr_dev NULL) or read by the
+// finalize kernel from the device scalar lr_dev.
+int step_impl(ark_opt_handle* h, float lr, const float* lr_dev, ark_opt_step_info* info) {
   DeviceGuard g(h->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   hipEvent_t* ev = nullptr;
@@ -393,7 +395,7 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
   }
   if (ev) ARK_HIP(hipEventRecord(ev[1], h->stream));
   ARK_HIP(ark::launch_finalize(h->fin_leaves, h->d_fold ? h->d_fold : h->d_part_sum, h->hp,
-                               lr, h->d_state, h->d_scal, h->d_info, h->stream));
+                               lr, lr_dev, h->d_state, h->d_scal, h->d_info, h->stream));
   if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
   if (h->nseg) {
     ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->d_segs, h->nseg, h->d_scal,
@@ -405,6 +407,29 @@ int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
   }
   if (info) return finish_info(h, info);
   return ARK_OPT_OK;
+}
+
+}  // namespace
+
+int ark_opt_step(ark_opt_handle* h, float lr, ark_opt_step_info* info) {
+  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
+  if (!finite_f(lr)) return fail(ARK_OPT_EINVAL, "lr must be finite");
+  return step_impl(h, lr, nullptr, info);
+}
+
+int ark_opt_step_lr_dev(ark_opt_handle* h, const float* lr_dev, ark_opt_step_info* info) {
+  if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
+  if (!lr_dev || ((uintptr_t)lr_dev & 3u))
+    return fail(ARK_OPT_EINVAL, "lr_dev is NULL or not 4-byte aligned");
+  int rc;
+  {
+    DeviceGuard g(h->device);
+    if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
+    if ((rc = check_buffer(lr_dev, 4, "lr_dev", 0))) return rc;
+  }
+  rc = step_impl(h, 0.0f, lr_dev, info);
+  if (rc == ARK_OPT_EINVAL) return fail(ARK_OPT_EINVAL, "the lr read from lr_dev is not finite");
+  return rc;
 }
 
 int ark_opt_record_overflow(ark_opt_handle* h, ark_opt_step_info* info) {

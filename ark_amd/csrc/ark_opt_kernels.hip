@@ -374,11 +374,14 @@ __device__ inline uint32_t amp_skip(const ark_opt_hparams& hp, ark_opt_state& st
 }
 
 // part_sum holds kFinThreads * L partials, zero past the last block's.
+// lr_ptr: when not NULL, this step's learning rate is *lr_ptr (read as the
+// kernel runs) instead of lr; a non-finite one makes the step a no-op that
+// reports ARK_OPT_EINVAL.
 template <int L>
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
     const double* __restrict__ part_sum, ark_opt_hparams hp, float lr,
-    ark_opt_state* __restrict__ state, StepScalars* __restrict__ scal,
-    ark_opt_step_info* __restrict__ info) {
+    const float* __restrict__ lr_ptr, ark_opt_state* __restrict__ state,
+    StepScalars* __restrict__ scal, ark_opt_step_info* __restrict__ info) {
   __shared__ double wsum[kFinThreads / 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -394,6 +397,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   for (int s = 0; s < log2i(kFinThreads / 64); ++s) y = y + __shfl_xor(y, 1 << s);
   if (lane != 0) return;
 
+  if (lr_ptr) lr = *lr_ptr;
   const double sumsq = y;
   const bool any_bad = __builtin_isnan(sumsq);
   ark_opt_state st = *state;
@@ -409,6 +413,10 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   if (st.early_stop) {
     out.status = ARK_OPT_EARLY_STOP;
     out.inv_scale = 1.0f / st.loss_scale;
+  } else if (!(fabsf(lr) <= 3.402823466e38f)) {  // a non-finite lr: nothing changes
+    out.status = ARK_OPT_EINVAL;
+    out.inv_scale = 1.0f / st.loss_scale;
+    sc.lr = 0.0f;
   } else {
     const float scale = st.loss_scale;
     const float inv = 1.0f / scale;  // training.rs:244
@@ -660,13 +668,13 @@ uint32_t finalize_leaves(uint32_t nparts) {
 }
 
 hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
-                           const ark_opt_hparams& hp, float lr,
+                           const ark_opt_hparams& hp, float lr, const float* lr_ptr,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream) {
   const dim3 grid(1), block(kFinThreads);
 #define ARK_FIN(L)                                                                   \
   hipLaunchKernelGGL((finalize_kernel<L>), grid, block, 0, stream, part_sum, hp, lr, \
-                     state, scal, info)
+                     lr_ptr, state, scal, info)
   switch (leaves) {
     case 1: ARK_FIN(1); break;
     case 2: ARK_FIN(2); break;

@@ -153,8 +153,9 @@ inline uint32_t sumsq_block_fast(const SegDesc* segs, uint64_t nseg, int spb, ui
 // partial buffer must hold kFinThreads * leaves doubles, zero past nparts.
 uint32_t finalize_leaves(uint32_t nparts);
 
+// lr_ptr: NULL, or a device scalar the kernel reads this step's lr from.
 hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
-                           const ark_opt_hparams& hp, float lr,
+                           const ark_opt_hparams& hp, float lr, const float* lr_ptr,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream);
 

@@ -118,6 +118,10 @@ extern "C" {
     /// `Optimizer::step_all` (`src/optimizer.rs:171-228`) with the AMP block of
     /// `Trainer::train_step` (`src/training.rs:289-326`).
     pub fn ark_opt_step(h: *mut ark_opt_handle, lr: f32, info: *mut ark_opt_step_info) -> c_int;
+    /// No reference counterpart: the step with lr read from a device scalar
+    /// (HIP graph replays that follow a schedule).
+    pub fn ark_opt_step_lr_dev(h: *mut ark_opt_handle, lr_dev: *const f32,
+                               info: *mut ark_opt_step_info) -> c_int;
     /// The logits-gradient skip (`src/training.rs:228-241`).
     pub fn ark_opt_record_overflow(h: *mut ark_opt_handle, info: *mut ark_opt_step_info) -> c_int;
     pub fn ark_opt_get_state(h: *mut ark_opt_handle, out: *mut ark_opt_state) -> c_int;

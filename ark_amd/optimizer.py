@@ -215,6 +215,19 @@ class Optimizer:
             return rc, out
         return check(lib().ark_opt_step(self._h, lr, None))
 
+    def step_lr_dev(self, lr_dev, info=False):
+        """One fused step whose lr the finalize kernel reads from the
+        one-element float32 GPU tensor lr_dev when it runs (graph replays
+        that follow a schedule).  Returns (status, StepInfo) when info is
+        True, else the status without waiting."""
+        import torch
+        assert lr_dev.is_cuda and lr_dev.dtype == torch.float32 and lr_dev.numel() == 1
+        if info:
+            out = _abi.StepInfo()
+            rc = check(lib().ark_opt_step_lr_dev(self._h, lr_dev.data_ptr(), C.byref(out)))
+            return rc, out
+        return check(lib().ark_opt_step_lr_dev(self._h, lr_dev.data_ptr(), None))
+
     def record_overflow(self, info=True):
         out = _abi.StepInfo()
         rc = check(lib().ark_opt_record_overflow(self._h, C.byref(out) if info else None))

@@ -176,12 +176,23 @@ int ark_opt_destroy(ark_opt_handle *h);
  * optimizer.rs:80-92, evaluated by the caller).  It travels as a kernel
  * argument: a HIP graph that captured a step replays the lr it was captured
  * with (t, the bias corrections and the AMP state still advance on the
- * device), so a schedule that changes lr needs a graph per lr value or a
- * fresh capture.  The step's norm pass reads the gradients, or the units the
+ * device), so a schedule that changes lr needs a graph per lr value, a
+ * fresh capture, or ark_opt_step_lr_dev.  The step's norm pass reads the gradients, or the units the
  * hand-off's final calls wrote (include/ark_grad.h) when they are fresh; a
  * capture keeps the choice it saw, so capture the step together with the
  * final calls that feed it, or with neither. */
 int ark_opt_step(ark_opt_handle *h, float lr, ark_opt_step_info *info);
+
+/* ark_opt_step with this step's learning rate read from the device scalar
+ * *lr_dev when the step's finalize kernel runs, instead of a host value.  No
+ * counterpart in the reference (its lr is a host value, Optimizer::lr_now,
+ * optimizer.rs:80-92); for steps replayed from a HIP graph: a captured call
+ * reads the scalar on every replay, so writing this step's lr into it
+ * (stream ordered before the replay) makes replays follow a schedule.  A
+ * non-finite value makes the step a no-op (state and buffers unchanged)
+ * whose info reports ARK_OPT_EINVAL, the status this call then returns when
+ * info is not NULL. */
+int ark_opt_step_lr_dev(ark_opt_handle *h, const float *lr_dev, ark_opt_step_info *info);
 
 /* The external skip path of training.rs:228-241: the caller found a
  * non-finite value upstream (the logits gradient) and drops this step.

@@ -56,3 +56,80 @@ def test_step_replays_match_eager(name):
                 it = torch.int16 if a.element_size() == 2 else torch.int32
                 assert torch.equal(a.view(it), b.view(it)), (k, i)
     og.close(), oe.close()
+
+
+def _same(pa, pb, n, what):
+    torch = _torch()
+    for i in range(n):
+        for a, b in ((pa.w(i), pb.w(i)), (pa.m(i), pb.m(i)), (pa.v(i), pb.v(i))):
+            it = torch.int16 if a.element_size() == 2 else torch.int32
+            assert torch.equal(a.view(it), b.view(it)), (what, i)
+
+
+def test_lr_from_a_device_scalar_follows_a_schedule_in_replays():
+    """ark_opt_step_lr_dev reads lr from a device scalar when the step runs:
+    eagerly it matches ark_opt_step with the same host lr bit for bit, and
+    one captured call replayed with the scalar rewritten (outside the graph)
+    before each replay follows a warmup-then-cosine schedule (lr_now,
+    optimizer.rs:80-92) exactly as eager steps with host lrs do."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    specs = config_tensors("c1")
+    sig = [1e-3] * len(specs)
+    scale, seed = 1024.0, 33
+    cfg = AdamConfig(lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0,
+                     warmup_steps=10)
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_max=2.0 ** 24)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        pg = H.gpu_problem(specs, seed, cfg.weight_decay, sig, scale)
+        pe = H.gpu_problem(specs, seed, cfg.weight_decay, sig, scale)
+        og, oe = Optimizer(cfg, pg, amp), Optimizer(cfg, pe, amp)
+        lr_dev = torch.zeros(1, dtype=torch.float32, device="cuda")
+    s.synchronize()
+    # eager: the device scalar and the host value give the same step
+    with torch.cuda.stream(s):
+        lr_dev.fill_(og.lr_now(1))
+        og.step_lr_dev(lr_dev)
+        oe.step_all(oe.lr_now(1))
+    s.synchronize()
+    _same(pg, pe, len(specs), "eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        og.step_lr_dev(lr_dev)
+    for k in range(2, 8):
+        lr = oe.lr_now(k)
+        with torch.cuda.stream(s):
+            H.gpu_regen_grads(pg, seed, sig, scale, k)
+            H.gpu_regen_grads(pe, seed, sig, scale, k)
+            lr_dev.fill_(lr)
+            g.replay()
+            oe.step_all(lr)
+        s.synchronize()
+        assert og.get_state().t == oe.get_state().t == k
+        _same(pg, pe, len(specs), k)
+    assert len({oe.lr_now(k) for k in range(2, 8)}) == 6  # the lr changed on every replay
+    og.close(), oe.close()
+
+
+def test_a_non_finite_device_lr_leaves_everything_as_it_was():
+    torch = _torch()
+    from ark_amd import _abi
+    from ark_amd._lib import ArkOptError
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    specs = config_tensors("c0")
+    p = H.gpu_problem(specs, 3, 0.1, [1e-3], 1024.0)
+    o = Optimizer(AdamConfig(), p, AmpConfig(loss_scale_init=1024.0))
+    before = [x.clone() for x in (p.w(0), p.m(0), p.v(0))]
+    st0 = o.get_state().as_dict()
+    lr_dev = torch.tensor([float("nan")], device="cuda")
+    with pytest.raises(ArkOptError, match="not finite"):
+        o.step_lr_dev(lr_dev, info=True)
+    torch.cuda.synchronize()
+    assert o.get_state().as_dict() == st0
+    for a, b in zip((p.w(0), p.m(0), p.v(0)), before):
+        assert torch.equal(a, b)
+    lr_dev.fill_(3e-4)
+    rc, info = o.step_lr_dev(lr_dev, info=True)
+    assert rc == _abi.OK and info.applied == 1 and info.lr == pytest.approx(3e-4)
+    o.close()
