@@ -494,6 +494,37 @@ int ark_opt_get_timing(ark_opt_handle* h, ark_opt_timing* out) {
   return ARK_OPT_OK;
 }
 
+int ark_hip_adam_step(float* w, const float* g, float* m, float* v, uint64_t n, float lr,
+                      float beta1, float beta2, float eps, float wd, uint32_t t, void* stream) {
+  if (n == 0) return ARK_OPT_OK;
+  if ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 3u))
+    return fail(ARK_OPT_EINVAL, "pointer not aligned to its element");
+  if (n > (1ull << 48) || (n + ark::kRow - 1) / ark::kRow * 64u >= (1ull << 32))
+    return fail(ARK_OPT_EINVAL, "n too large (%llu)", (unsigned long long)n);
+  int rc;
+  const uintptr_t uw = (uintptr_t)w, ug = (uintptr_t)g, um = (uintptr_t)m, uv = (uintptr_t)v;
+  if ((rc = ark::check_disjoint({{uw, uw + n * 4u, "w", 0}, {um, um + n * 4u, "m", 0},
+                                 {uv, uv + n * 4u, "v", 0}},
+                                {{ug, ug + n * 4u, "g", 0}})))
+    return rc;
+  if ((rc = check_buffer(w, n * 4u, "w", 0))) return rc;
+  if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
+  if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;
+  if ((rc = check_buffer(v, n * 4u, "v", 0))) return rc;
+  const bool vec = (((uw | ug | um | uv) & 15u) == 0);
+  StepScalars sc{};
+  sc.applied = 1u;
+  sc.inv = 1.0f;
+  sc.coef = 1.0f;
+  sc.lr = lr;
+  sc.lr_eff = ark::lr_eff_of(lr, beta1, beta2, t);  // opti.s:38-90
+  sc.c1 = 1.0f - beta1;                              // opti.s:94-96
+  sc.c2 = 1.0f - beta2;                              // opti.s:97-99
+  ARK_HIP(ark::launch_adamw_single_w32(w, g, m, v, n, wd, vec, sc, beta1, beta2, eps,
+                                        (hipStream_t)stream));
+  return ARK_OPT_OK;
+}
+
 int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
                           uint64_t n, float lr, float beta1, float beta2,
                           float eps, float wd, uint32_t t, void* stream) {

@@ -500,6 +500,27 @@ __device__ __forceinline__ uint32_t adam_elem(uint32_t w16, float g, float& m,
   return f2h(w);                      // fcvtn
 }
 
+// One element of _ark_asm_adam_step (opti.s:105-131; the tail :135-160 is
+// the same sequence): adam_elem's operations on an fp32 weight, without the
+// fp16 widening and narrowing.
+__device__ __forceinline__ float adam_elem_w32(float w, float g, float& m, float& v,
+                                               const ElemConsts& k) {
+  float mm = m * k.beta1;             // fmul  :114
+  mm = __builtin_fmaf(k.c1, g, mm);   // fmla  :115
+  float vv = v * k.beta2;             // fmul  :118
+  const float gg = g * g;             // fmul  :119
+  vv = __builtin_fmaf(k.c2, gg, vv);  // fmla  :120
+  float d = sqrtf(vv);                // fsqrt :123
+  d = d + k.eps;                      // fadd  :124
+  float u = mm / d;                   // fdiv  :125
+  u = u * k.lr_eff;                   // fmul  :126
+  w = w * k.decay;                    // fmul  :128
+  w = w - u;                          // fsub  :129
+  m = mm;
+  v = vv;
+  return w;
+}
+
 // The elements [0, valid) of one 256-element row, one wave: lane l owns
 // [4l, 4l + 4).  Full aligned rows use one coalesced access per array.
 template <typename GT>
@@ -587,6 +608,50 @@ __global__ __launch_bounds__(64) void adamw_single_kernel(
   c.lr_eff = sc.lr_eff;
   c.decay = 1.0f - sc.lr * wd;
   adam_row<float>(w + r0, g + r0, m + r0, v + r0, valid, vec != 0, 1.0f, 1.0f, c);
+}
+
+// ark_hip_adam_step: one wave per 256-element row of an fp32-weight tensor,
+// lane l on elements [4l, 4l + 4), one 16-byte access per array when the row
+// is full and every pointer 16-byte aligned.
+__global__ __launch_bounds__(64) void adamw_single_w32_kernel(
+    float* w, const float* g, float* m, float* v, uint64_t n, float wd, uint32_t vec,
+    StepScalars sc, float beta1, float beta2, float eps) {
+  const uint64_t r0 = (uint64_t)blockIdx.x * kRow;
+  const uint32_t valid = n - r0 < (uint64_t)kRow ? (uint32_t)(n - r0) : (uint32_t)kRow;
+  ElemConsts c;
+  c.beta1 = beta1;
+  c.beta2 = beta2;
+  c.c1 = sc.c1;
+  c.c2 = sc.c2;
+  c.eps = eps;
+  c.lr_eff = sc.lr_eff;
+  c.decay = 1.0f - sc.lr * wd;
+  const uint64_t e = r0 + threadIdx.x * 4u;
+  if (vec && valid == (uint32_t)kRow) {
+    const f32x4 gr = ld_nt<f32x4>(g + e);
+    const f32x4 wr = ld_nt<f32x4>(w + e);
+    const f32x4 mr = ld_nt<f32x4>(m + e);
+    const f32x4 vr = ld_nt<f32x4>(v + e);
+    const float gf[4] = {gr.x, gr.y, gr.z, gr.w};
+    float ww[4] = {wr.x, wr.y, wr.z, wr.w};
+    float mm[4] = {mr.x, mr.y, mr.z, mr.w};
+    float vv[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ww[j] = adam_elem_w32(ww[j], gf[j], mm[j], vv[j], c);
+    st_nt<f32x4>(w + e, f32x4{ww[0], ww[1], ww[2], ww[3]});
+    st_nt<f32x4>(m + e, f32x4{mm[0], mm[1], mm[2], mm[3]});
+    st_nt<f32x4>(v + e, f32x4{vv[0], vv[1], vv[2], vv[3]});
+  } else {
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint64_t i = e + j;
+      if (i >= r0 + valid) break;
+      float mj = ld_g<float>(m + i), vj = ld_g<float>(v + i);
+      const float wj = adam_elem_w32(ld_g<float>(w + i), ld_g<float>(g + i), mj, vj, c);
+      st_g<float>(w + i, wj);
+      st_g<float>(m + i, mj);
+      st_g<float>(v + i, vj);
+    }
+  }
 }
 
 }  // namespace
@@ -712,6 +777,17 @@ hipError_t launch_adamw_single(uint16_t* w, const float* g, float* m, float* v,
   if (rows * 64u >= (1ull << 32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(adamw_single_kernel, dim3((uint32_t)rows), dim3(64), 0, stream, w,
                      g, m, v, n, wd, vec ? 1u : 0u, sc, beta1, beta2, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw_single_w32(float* w, const float* g, float* m, float* v, uint64_t n,
+                                   float wd, bool vec, const StepScalars& sc, float beta1,
+                                   float beta2, float eps, hipStream_t stream) {
+  const uint64_t rows = (n + kRow - 1) / kRow;
+  if (rows == 0) return hipSuccess;
+  if (rows * 64u >= (1ull << 32)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(adamw_single_w32_kernel, dim3((uint32_t)rows), dim3(64), 0, stream, w, g,
+                     m, v, n, wd, vec ? 1u : 0u, sc, beta1, beta2, eps);
   return hipGetLastError();
 }
 

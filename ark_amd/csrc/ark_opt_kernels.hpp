@@ -171,6 +171,12 @@ hipError_t launch_adamw_single(uint16_t* w, const float* g, float* m, float* v,
                                const StepScalars& sc, float beta1, float beta2,
                                float eps, hipStream_t stream);
 
+// The same for an fp32-weight tensor: the drop-in of one ark_asm_adam_step
+// call (opti.s:20-177).
+hipError_t launch_adamw_single_w32(float* w, const float* g, float* m, float* v, uint64_t n,
+                                   float wd, bool vec, const StepScalars& sc, float beta1,
+                                   float beta2, float eps, hipStream_t stream);
+
 hipError_t launch_record_overflow(const ark_opt_hparams& hp,
                                   ark_opt_state* state,
                                   ark_opt_step_info* info, hipStream_t stream);

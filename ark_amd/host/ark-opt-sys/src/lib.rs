@@ -128,6 +128,11 @@ extern "C" {
     pub fn ark_opt_set_state(h: *mut ark_opt_handle, st: *const ark_opt_state) -> c_int;
     pub fn ark_opt_set_timing(h: *mut ark_opt_handle, enable: c_int) -> c_int;
     pub fn ark_opt_get_timing(h: *mut ark_opt_handle, out: *mut ark_opt_timing) -> c_int;
+    /// `ark_asm_adam_step` (`asm/opti.s:20-177`, `src/ffi.rs:98-101`), fp32
+    /// weights, plus a stream.
+    pub fn ark_hip_adam_step(w: *mut f32, g: *const f32, m: *mut f32, v: *mut f32, n: u64,
+                             lr: f32, beta1: f32, beta2: f32, eps: f32, wd: f32, t: u32,
+                             stream: *mut c_void) -> c_int;
     /// `ark_asm_adam_step_f16` (`asm/opti.s:189-193`, `src/optimizer.rs:20-23`)
     /// plus a stream.
     pub fn ark_hip_adam_step_f16(w: *mut u16, g: *const f32, m: *mut f32, v: *mut f32, n: u64,

@@ -211,6 +211,15 @@ int ark_opt_set_state(ark_opt_handle *h, const ark_opt_state *st);
 int ark_opt_set_timing(ark_opt_handle *h, int enable);
 int ark_opt_get_timing(ark_opt_handle *h, ark_opt_timing *out);
 
+/* Drop-in for one call of ark_asm_adam_step (opti.s:20-177, declared at
+ * ffi.rs:98-101), the reference's fp32-weight kernel (unused by its trainer):
+ * the same arguments in the same order plus the stream, fp32 weights and
+ * gradients used as given, t == 0 treated as 1.  One wave per 256-element
+ * row, the element sequence of ark_hip_adam_step_f16 without the fp16
+ * conversions; w, m, v and g must not share a byte. */
+int ark_hip_adam_step(float *w, const float *g, float *m, float *v, uint64_t n, float lr,
+                      float beta1, float beta2, float eps, float wd, uint32_t t, void *stream);
+
 /* Drop-in for one call of ark_asm_adam_step_f16 (opti.s:189-193, declared
  * at optimizer.rs:20-23 and ffi.rs:105-108): same arguments in the same
  * order, fp32 gradients used as given (no unscale, no clip), t == 0 treated

@@ -66,6 +66,8 @@ def lib():
     L.ark_ref_pow_binary.restype = C.c_float
     L.ark_ref_prologue.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float,
                                    C.c_uint32, C.POINTER(Scalars)]
+    L.ark_ref_adam_step_f32.argtypes = [P, P, P, P, C.c_uint64, C.c_float, C.c_float,
+                                        C.c_float, C.c_float, C.c_float, C.c_uint32]
     L.ark_ref_adam_step_f16.argtypes = [P, P, P, P, C.c_uint64, C.c_float, C.c_float,
                                         C.c_float, C.c_float, C.c_float, C.c_uint32]
     L.ark_ref_sumsq.argtypes = [C.POINTER(_abi.Tensor), C.c_int32, C.c_uint32, C.c_float,
@@ -174,6 +176,15 @@ def adam_step_f16(w, g, m, v, lr, beta1, beta2, eps, wd, t):
         assert a.dtype == dt and a.flags.c_contiguous
     assert w.size == g.size == m.size == v.size
     lib().ark_ref_adam_step_f16(_ptr(w), _ptr(g), _ptr(m), _ptr(v), w.size, lr, beta1,
+                                beta2, eps, wd, t)
+
+
+def adam_step_f32(w, g, m, v, lr, beta1, beta2, eps, wd, t):
+    """In place on float32 numpy arrays (opti.s:20-177, fp32 weights)."""
+    for a in (w, g, m, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    assert w.size == g.size == m.size == v.size
+    lib().ark_ref_adam_step_f32(_ptr(w), _ptr(g), _ptr(m), _ptr(v), w.size, lr, beta1,
                                 beta2, eps, wd, t)
 
 

@@ -308,6 +308,37 @@ static inline uint16_t adam_elem(uint16_t w16, float g, float *m, float *v,
   return ark_ref_f32_to_f16(w);      /* fcvtn v7.4h, v3.4s   :307 */
 }
 
+/* One element of _ark_asm_adam_step (opti.s:105-131; the scalar tail
+ * :135-160 performs the identical sequence): the fp16 element's operations
+ * on fp32 weights, without the two conversions. */
+static inline float adam_elem_f32(float w, float g, float *m, float *v,
+                                  const ark_ref_scalars *s, float beta1,
+                                  float beta2, float eps) {
+  float mm = *m * beta1;             /* fmul v1, v1, v16     :114 */
+  mm = fmaf(s->c1, g, mm);           /* fmla v1, v18, v0     :115 */
+  float vv = *v * beta2;             /* fmul v2, v2, v17     :118 */
+  float gg = g * g;                  /* fmul v4, v0, v0      :119 */
+  vv = fmaf(s->c2, gg, vv);          /* fmla v2, v19, v4     :120 */
+  float d = sqrtf(vv);               /* fsqrt v5, v2         :123 */
+  d = d + eps;                       /* fadd v5, v5, v20     :124 */
+  float u = mm / d;                  /* fdiv v6, v1, v5      :125 */
+  u = u * s->lr_eff;                 /* fmul v6, v6, v21     :126 */
+  w = w * s->decay;                  /* fmul v3, v3, v22     :128 */
+  w = w - u;                         /* fsub v3, v3, v6      :129 */
+  *m = mm;                           /* str q1               :116 */
+  *v = vv;                           /* str q2               :121 */
+  return w;                          /* str q3               :130 */
+}
+
+void ark_ref_adam_step_f32(float *w, const float *g, float *m, float *v, uint64_t n,
+                           float lr, float beta1, float beta2, float eps, float wd,
+                           uint32_t t) {
+  ark_ref_scalars s;
+  ark_ref_prologue(lr, beta1, beta2, wd, t, &s); /* opti.s:38-103, as :210-271 */
+  for (uint64_t i = 0; i < n; ++i)
+    w[i] = adam_elem_f32(w[i], g[i], &m[i], &v[i], &s, beta1, beta2, eps);
+}
+
 void ark_ref_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
                            uint64_t n, float lr, float beta1, float beta2,
                            float eps, float wd, uint32_t t) {

@@ -65,6 +65,12 @@ void ark_ref_prologue(float lr, float beta1, float beta2, float wd, uint32_t t,
  * restatement.  Returns the mode in effect (0 without AVX2/F16C/FMA). */
 int ark_ref_set_vector(int on);
 
+/* Exact transliteration of ark_asm_adam_step (opti.s:20-177): fp32 weights,
+ * the same prologue and element sequence without the fp16 conversions. */
+void ark_ref_adam_step_f32(float *w, const float *g, float *m, float *v, uint64_t n,
+                           float lr, float beta1, float beta2, float eps, float wd,
+                           uint32_t t);
+
 /* Exact transliteration of ark_asm_adam_step_f16 (opti.s:192-360). */
 void ark_ref_adam_step_f16(uint16_t *w, const float *g, float *m, float *v,
                            uint64_t n, float lr, float beta1, float beta2,

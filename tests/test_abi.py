@@ -137,6 +137,23 @@ def test_single_tensor_dropin_rejects_aliased_buffers():
     assert "overlaps" not in msg()
 
 
+def test_fp32_weight_dropin_argument_checks():
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    args = (3e-4, 0.9, 0.999, 1e-8, 0.01, 1, None)
+    assert L.ark_hip_adam_step(None, None, None, None, 0, *args) == _abi.OK
+    assert L.ark_hip_adam_step(0x1002, 0x2000, 0x3000, 0x4000, 10, *args) == _abi.EINVAL
+    assert "aligned" in msg()
+    for n in (2 ** 64 - 1, 2 ** 48 + 1):
+        assert L.ark_hip_adam_step(0x1000, 0x2000, 0x3000, 0x4000, n, *args) == _abi.EINVAL
+        assert "too large" in msg()
+    # fp32 w spans 4 B per element: w at 1 MiB reaches into m placed 3996 B on
+    assert L.ark_hip_adam_step(1 * MB, 2 * MB, 1 * MB + 3996, 3 * MB, 1000, *args) == _abi.EINVAL
+    assert "overlaps" in msg() and "0 w" in msg() and "0 m" in msg(), msg()
+    assert L.ark_hip_adam_step(1 * MB, 2 * MB, 1 * MB + 4000, 3 * MB, 1000, *args) != _abi.OK
+    assert "overlaps" not in msg()
+
+
 def test_single_tensor_dropin_argument_checks():
     L = _lib.lib()
     assert L.ark_hip_adam_step_f16(None, None, None, None, 0, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1,

@@ -343,6 +343,66 @@ def test_single_tensor_dropin_matches_reference_kernel():
         assert not np.any(H.bits_differ32(dv.cpu().numpy()[off:], vv))
 
 
+def _w32_step(torch, w, g, m, v, off, n, lr, b1, b2, eps, wd, t):
+    from ark_amd._lib import check, lib
+    check(lib().ark_hip_adam_step(
+        w.data_ptr() + 4 * off, g.data_ptr() + 4 * off, m.data_ptr() + 4 * off,
+        v.data_ptr() + 4 * off, n, lr, b1, b2, eps, wd, t,
+        C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+
+
+@pytest.mark.parametrize("n,off", [(1, 0), (3, 1), (255, 0), (257, 2), (4096 * 3 + 5, 0),
+                                   (10000, 3), (768 * 768, 0)])
+def test_fp32_weight_dropin_matches_reference_kernel(n, off):
+    """ark_hip_adam_step = successive ark_asm_adam_step calls (opti.s:20-177):
+    ten steps from t = 0 (treated as 1) with a new gradient each, the c0
+    tensor shape (768 x 768) among ragged sizes; offsets of 1-3 elements take
+    the per-element path, aligned full rows the 16-byte one."""
+    torch = _torch()
+    rng = np.random.default_rng(n * 7 + off)
+    w = (rng.standard_normal(n + off) * 0.02).astype(np.float32)
+    m = np.zeros(n + off, np.float32)
+    v = np.zeros(n + off, np.float32)
+    dw, dm, dv = (torch.from_numpy(a.copy()).cuda() for a in (w, m, v))
+    ww, mm, vv = w[off:].copy(), m[off:].copy(), v[off:].copy()
+    for t in range(10):
+        g = (rng.standard_normal(n + off) * 10.0 ** rng.uniform(-5, 0)).astype(np.float32)
+        dg = torch.from_numpy(g).cuda()
+        _w32_step(torch, dw, dg, dm, dv, off, n, 6e-4, 0.9, 0.95, 1e-8, 0.1, t)
+        oracle.adam_step_f32(ww, g[off:].copy(), mm, vv, 6e-4, 0.9, 0.95, 1e-8, 0.1, t)
+    torch.cuda.synchronize()
+    for d, h in ((dw, ww), (dm, mm), (dv, vv)):
+        got = d.cpu().numpy()
+        assert not np.any(H.bits_differ32(got[off:], h)), n
+    # the element before the span is untouched
+    assert np.array_equal(dw.cpu().numpy()[:off], w[:off])
+
+
+def test_fp32_weight_dropin_special_values():
+    """Subnormal, huge, infinite and NaN gradients and weights, zero moments
+    and eps = 0 (0/0 -> NaN), through both the 16-byte and the per-element
+    paths: the same results as the reference kernel, NaN for NaN."""
+    torch = _torch()
+    vals = np.array([0.0, -0.0, 1e-45, -1e-40, 1e-20, 3e38, -3e38, np.inf, -np.inf, np.nan,
+                     1.0, -1.0, 65504.0, 2.0 ** -126], np.float32)
+    rng = np.random.default_rng(5)
+    n = 1024 + 37
+    for eps in (1e-8, 0.0):
+        w = rng.choice(vals, n).astype(np.float32)
+        g = rng.choice(vals, n).astype(np.float32)
+        m = rng.choice(vals[:7], n).astype(np.float32)
+        v = np.abs(rng.choice(vals[:7], n)).astype(np.float32)
+        for off in (0, 1):
+            dw, dg, dm, dv = (torch.from_numpy(a.copy()).cuda() for a in (w, g, m, v))
+            k = n - off
+            _w32_step(torch, dw, dg, dm, dv, off, k, 1e-3, 0.9, 0.999, eps, 0.01, 3)
+            ww, mm, vv = w[off:].copy(), m[off:].copy(), v[off:].copy()
+            oracle.adam_step_f32(ww, g[off:].copy(), mm, vv, 1e-3, 0.9, 0.999, eps, 0.01, 3)
+            torch.cuda.synchronize()
+            for d, h in ((dw, ww), (dm, mm), (dv, vv)):
+                assert not np.any(H.bits_differ32(d.cpu().numpy()[off:], h)), (eps, off)
+
+
 @pytest.mark.parametrize("true_grads,clipped", [
     ([0.5, -0.5, 0.5, 0.5], 0),          # norm exactly 1.0 = grad_clip: `>` is strict
     ([1.0 + 2.0 ** -10], 1),             # just above: coef = 1 / norm

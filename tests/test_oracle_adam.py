@@ -209,3 +209,77 @@ def test_zero_betas_reduce_to_sign_sgd():
     got = ww.view(np.float16).astype(np.float64)
     ulp = np.spacing(np.abs(expect).astype(np.float16)).astype(np.float64)
     assert np.all(np.abs(got - expect) <= ulp)
+
+
+# ---- the fp32-weight kernel (ark_asm_adam_step, opti.s:20-177) --------------
+
+def py_adam_elem_f32(w, g, m, v, s, b1, b2, eps):
+    """The fp32-weight element: py_adam_elem's operations on an fp32 weight,
+    without the fp16 widening and narrowing (opti.s:114-130)."""
+    b1, b2, eps = F32(b1), F32(b2), F32(eps)
+    mm = fma32(s["c1"], g, F32(F32(m) * b1))
+    vv = fma32(s["c2"], F32(F32(g) * F32(g)), F32(F32(v) * b2))
+    d = F32(np.sqrt(vv) + eps)
+    u = F32(F32(mm / d) * s["lr_eff"])
+    return F32(F32(F32(w) * s["decay"]) - u), mm, vv
+
+
+@pytest.mark.parametrize("t", [0, 1, 7, 123457])
+def test_fp32_weight_step_second_restatement_bit_exact(t):
+    """Weights the fp16 path never sees (fp32 values between fp16 ones,
+    fp32 subnormals, beyond 65504) against the independent restatement."""
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-8, 0.1
+    _, g, m, v = _random_inputs(1200, 1000 + t)
+    rng = np.random.default_rng(t)
+    w = (rng.standard_normal(g.size) * 10.0 ** rng.integers(-40, 6, g.size)).astype(np.float32)
+    w[::13] = np.float32(1e-41)
+    w[::17] = np.float32(1e6)
+    s = py_prologue(lr, b1, b2, wd, t)
+    ow, om, ov = w.copy(), m.copy(), v.copy()
+    oracle.adam_step_f32(ow, g, om, ov, lr, b1, b2, eps, wd, t)
+    for i in range(w.size):
+        pw, pm, pv = py_adam_elem_f32(w[i], g[i], m[i], v[i], s, b1, b2, eps)
+        assert ow[i].view(np.uint32) == F32(pw).view(np.uint32), (i, ow[i], pw)
+        assert om[i].view(np.uint32) == F32(pm).view(np.uint32), i
+        assert ov[i].view(np.uint32) == F32(pv).view(np.uint32), i
+
+
+@pytest.mark.parametrize("t", [1, 50])
+def test_fp32_weight_step_is_the_fp16_step_before_its_rounding(t):
+    """On weights fp16 can hold, the fp16 kernel is the fp32 kernel followed
+    by fcvtn: the same m and v bits, and the fp16 weight equal to the fp32
+    weight rounded to nearest even (both restatements run in the oracle's C
+    code, against each other)."""
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-8, 0.1
+    w16, g, m, v = _random_inputs(4000, 77 + t)
+    w32 = w16.view(np.float16).astype(np.float32)
+    a_w, a_m, a_v = w16.copy(), m.copy(), v.copy()
+    b_w, b_m, b_v = w32.copy(), m.copy(), v.copy()
+    oracle.adam_step_f16(a_w, g, a_m, a_v, lr, b1, b2, eps, wd, t)
+    oracle.adam_step_f32(b_w, g, b_m, b_v, lr, b1, b2, eps, wd, t)
+    np.testing.assert_array_equal(a_m.view(np.uint32), b_m.view(np.uint32))
+    np.testing.assert_array_equal(a_v.view(np.uint32), b_v.view(np.uint32))
+    np.testing.assert_array_equal(a_w, oracle.f32_to_f16(b_w))
+    # and the fp32 result is not merely the fp16 one widened
+    assert (b_w != a_w.view(np.float16).astype(np.float32)).mean() > 0.5
+
+
+def test_fp32_weight_step_closed_forms():
+    """Zero gradient and state: w * decay exactly (lr 3e-4, wd 0.1); wd 0:
+    decay exactly 1; first step from zero state: u = lr_eff * c1 g /
+    (sqrt(c2 g^2) + eps)."""
+    w = np.array([1.0, -3.5, 1e-30, 7e5], np.float32)
+    z = np.zeros(4, np.float32)
+    ow = w.copy()
+    oracle.adam_step_f32(ow, z.copy(), z.copy(), z.copy(), 3e-4, 0.9, 0.95, 1e-8, 0.1, 1)
+    decay = F32(F32(1.0) - F32(F32(3e-4) * F32(0.1)))
+    np.testing.assert_array_equal(ow, (w * decay).astype(np.float32))
+    g = np.array([1e-3, -2e-2, 5.0, 0.0], np.float32)
+    ow, om, ov = w.copy(), z.copy(), z.copy()
+    oracle.adam_step_f32(ow, g, om, ov, 3e-4, 0.9, 0.95, 1e-8, 0.0, 1)
+    s = py_prologue(3e-4, 0.9, 0.95, 0.0, 1)
+    for i in range(4):
+        mm = fma32(s["c1"], g[i], F32(0.0))
+        vv = fma32(s["c2"], F32(g[i] * g[i]), F32(0.0))
+        u = F32(F32(mm / F32(np.sqrt(vv) + F32(1e-8))) * s["lr_eff"])
+        assert ow[i] == F32(w[i] - u), i

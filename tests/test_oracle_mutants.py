@@ -26,16 +26,25 @@ CFLAGS = ["-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-math-errno", "-
 # name: (text in ark_oracle.c, planted replacement, pin files tests/test_oracle_<x>.py)
 MUTANTS = {
     # AdamW element update and prologue (opti.s:210-308)
-    "first_moment_takes_beta2": ("float mm = *m * beta1;", "float mm = *m * beta2;", ["adam"]),
-    "second_moment_drops_the_square": ("vv = fmaf(s->c2, gg, vv);", "vv = fmaf(s->c2, g, vv);",
-                                       ["adam"]),
-    "first_moment_not_fused": ("mm = fmaf(s->c1, g, mm);", "mm = s->c1 * g + mm;", ["adam"]),
-    "eps_inside_the_root": ("d = d + eps;", "d = sqrtf(vv + eps);", ["adam"]),
-    "update_not_scaled": ("u = u * s->lr_eff;", "u = u * s->c1;", ["adam"]),
+    "first_moment_takes_beta2": ('float mm = *m * beta1;             /* fmul v1, v1, v16     :286 */',
+        'float mm = *m * beta2;             /* fmul v1, v1, v16     :286 */', ["adam"]),
+    "second_moment_drops_the_square": ('vv = fmaf(s->c2, gg, vv);          /* fmla v2, v19, v4     :293 */',
+        'vv = fmaf(s->c2, g, vv);          /* fmla v2, v19, v4     :293 */', ["adam"]),
+    "first_moment_not_fused": ('mm = fmaf(s->c1, g, mm);           /* fmla v1, v18, v0     :287 */',
+        'mm = s->c1 * g + mm;           /* fmla v1, v18, v0     :287 */', ["adam"]),
+    "eps_inside_the_root": ('d = d + eps;                       /* fadd v5, v5, v20     :298 */',
+        'd = sqrtf(vv + eps);                       /* fadd v5, v5, v20     :298 */', ["adam"]),
+    "update_not_scaled": ('u = u * s->lr_eff;                 /* fmul v6, v6, v21     :300 */',
+        'u = u * s->c1;                 /* fmul v6, v6, v21     :300 */', ["adam"]),
     "decay_sign": ("out->decay = 1.0f - lw;", "out->decay = 1.0f + lw;", ["adam"]),
     "bias_correction_without_root": ("float r = sqrtf(out->bc2);", "float r = out->bc2;",
                                      ["adam"]),
     "t0_not_coerced": ("if (t == 0) t = 1;", "if (t == 0) t = 0;", ["adam"]),
+    # the fp32-weight element (opti.s:105-131)
+    "fp32_weight_decay_skipped": ('w = w * s->decay;                  /* fmul v3, v3, v22     :128 */',
+        'w = w * 1.0f;                  /* fmul v3, v3, v22     :128 */', ["adam"]),
+    "fp32_first_moment_not_fused": ('mm = fmaf(s->c1, g, mm);           /* fmla v1, v18, v0     :115 */',
+        'mm = s->c1 * g + mm;           /* fmla v1, v18, v0     :115 */', ["adam"]),
     "power_multiplies_beta": ("if (k & 1u) res = res * base;", "if (k & 1u) res = res * beta;",
                               ["adam"]),
     # norm and finite flag (optimizer.rs:127-145, training.rs:291)
