@@ -669,7 +669,10 @@ def run_dropin(a):
     here ark_hip_adam_step_f16 is launched 272 times per step over EKO-237M
     with fp32 gradients (24 B/param: g 4, w 2+2, m 4+4, v 4+4), no unscale
     or clip.  One step's launches are captured in a HIP graph and replayed,
-    so the figure is the kernels', not Python's launch loop."""
+    so the figure is the kernels', not Python's launch loop.  With --weights
+    f32 the same pattern runs ark_hip_adam_step (ark_asm_adam_step,
+    opti.s:20-177) over fp32 copies of the weights: 28 B/param (g 4, w 4+4,
+    m 4+4, v 4+4)."""
     import ctypes as C
     import numpy as np
     import torch
@@ -682,16 +685,21 @@ def run_dropin(a):
     with torch.cuda.stream(stream):
         ps = synth.problem(specs, SEED, HP["weight_decay"], [1e-3] * len(specs), 1.0,
                            grad_dtype=_abi.GRAD_F32)
+        w32 = [ps.w(i).float() for i in range(len(specs))] if a.weights == "f32" else None
     n = ps.n_params
     L = lib()
     sp = C.c_void_p(stream.cuda_stream)
-    calls = [(ps.w(i).data_ptr(), ps.g(i).data_ptr(), ps.m(i).data_ptr(), ps.v(i).data_ptr(),
-              s.n, HP["weight_decay"] if s.decay else 0.0) for i, s in enumerate(specs)]
+    fn, bpp, kname, entry = ((L.ark_hip_adam_step, 28, "adamw_single_w32_kernel",
+                              "ark_hip_adam_step") if w32 else
+                             (L.ark_hip_adam_step_f16, 24, "adamw_single_kernel",
+                              "ark_hip_adam_step_f16"))
+    calls = [((w32[i] if w32 else ps.w(i)).data_ptr(), ps.g(i).data_ptr(), ps.m(i).data_ptr(),
+              ps.v(i).data_ptr(), s.n, HP["weight_decay"] if s.decay else 0.0)
+             for i, s in enumerate(specs)]
 
     def step(t):
         for w, g, m, v, nn, wd in calls:
-            rc = L.ark_hip_adam_step_f16(w, g, m, v, nn, HP["lr"], HP["beta1"], HP["beta2"],
-                                         HP["eps"], wd, t, sp)
+            rc = fn(w, g, m, v, nn, HP["lr"], HP["beta1"], HP["beta2"], HP["eps"], wd, t, sp)
             if rc:
                 check(rc)
 
@@ -719,34 +727,39 @@ def run_dropin(a):
         from concurrent.futures import ThreadPoolExecutor
         th = a.cpu_threads or min(16, os.cpu_count() or 1)
         e = [s.name for s in specs].index("embed")
-        hw = ps.w(e).view(torch.int16).cpu().numpy().view(np.uint16).copy()
         hg = ps.g(e).cpu().numpy().copy()
+        if w32:
+            hw = w32[e].cpu().numpy().copy()
+            ref = oracle.adam_step_f32
+        else:
+            hw = ps.w(e).view(torch.int16).cpu().numpy().view(np.uint16).copy()
+            ref = oracle.adam_step_f16
         hm, hv = np.zeros_like(hg), np.zeros_like(hg)
         parts = list(zip(*(np.array_split(x, th) for x in (hw, hg, hm, hv))))
         reps, t0 = 0, time.perf_counter()
         with ThreadPoolExecutor(th) as ex:
             while time.perf_counter() - t0 < min(a.cpu_seconds, 10.0):
-                list(ex.map(lambda p: oracle.adam_step_f16(*p, HP["lr"], HP["beta1"],
-                                                           HP["beta2"], HP["eps"],
-                                                           HP["weight_decay"], 3), parts))
+                list(ex.map(lambda p: ref(*p, HP["lr"], HP["beta1"], HP["beta2"], HP["eps"],
+                                          HP["weight_decay"], 3), parts))
                 reps += 1
         el = time.perf_counter() - t0
-        cpu = dict(value=round(24 * hw.size * reps / el / 1e9, 3), unit="GB/s", cores=th,
-                   kind="port", sample=f"{reps} ark_asm_adam_step_f16 restatements over the "
-                   f"{hw.size}-element embedding in {el:.1f} s on {th} threads")
-    gbs = 24 * n / (ms * 1e-3) / 1e9
+        cpu = dict(value=round(bpp * hw.size * reps / el / 1e9, 3), unit="GB/s", cores=th,
+                   kind="port", sample=f"{reps} {entry.replace('hip', 'asm')} restatements over "
+                   f"the {hw.size}-element embedding in {el:.1f} s on {th} threads")
+    gbs = bpp * n / (ms * 1e-3) / 1e9
+    wdesc = "fp32 weights" if w32 else "fp16 weights"
     out = {
-        "metric": "EKO-237M reference call pattern: 272 ark_hip_adam_step_f16 launches per step, "
+        "metric": f"EKO-237M reference call pattern: 272 {entry} launches per step, "
                   "GB/s (1 GPU)",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "dropin: 272 single-tensor launches over EKO-237M, fp32 "
-                               "gradients, replayed as one HIP graph",
-                   "params": n, "bytes_per_step": 24 * n},
-        "roofline": {"kernel": "adamw_single_kernel", "bound": "hbm", "achieved": round(gbs, 2),
+        "config": {"workload": f"dropin: 272 single-tensor launches over EKO-237M, {wdesc}, "
+                               "fp32 gradients, replayed as one HIP graph",
+                   "params": n, "bytes_per_step": bpp * n},
+        "roofline": {"kernel": kname, "bound": "hbm", "achieved": round(gbs, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": 24 * n},
+                     "traffic": None, "algorithmic_bytes_per_launch": bpp * n},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -772,6 +785,9 @@ def main():
                          "configurations; f32, as the gradient hand-off produces; f32-fused, "
                          "produced by the hand-off's final accumulation, which also forms the "
                          "norm's first level so the step does not re-read the gradients)")
+    ap.add_argument("--weights", default="f16", choices=["f16", "f32"],
+                    help="dropin: fp16 weights (ark_hip_adam_step_f16, the trainer's call) or "
+                         "fp32 weights (ark_hip_adam_step)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
