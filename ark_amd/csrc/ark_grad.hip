@@ -585,6 +585,10 @@ __global__ __launch_bounds__(kTileCols) void run_kernel(float* __restrict__ g, u
 }
 
 constexpr uint64_t kMaxFlatBlocks = 1u << 20;
+// gather_kernel and run_kernel launch one 256-lane block per token along x,
+// and a launch's work-items along one dimension must stay below 2^32.
+constexpr uint32_t kMaxTokens = (uint32_t)((1ull << 32) / kThreads) - 1u;  // 16,777,215
+static_assert(kTileCols == kThreads, "both per-token launches use 256-lane blocks");
 
 using ark::overlaps;
 
@@ -623,7 +627,9 @@ int scatter_check(const float* embed_grad, uint32_t vocab, uint32_t d, const uin
   *skip = batch_seq == 0 || d == 0;
   if (*skip) return ARK_OPT_OK;
   if (vocab == 0) return fail(ARK_OPT_EINVAL, "vocab is 0");
-  if (batch_seq > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "batch_seq too large");
+  if (batch_seq > kMaxTokens)
+    return fail(ARK_OPT_EINVAL, "batch_seq = %u too large (at most %u tokens per call)", batch_seq,
+                kMaxTokens);
   if (((uint64_t)d + kTileCols - 1) / kTileCols > 65535u) return fail(ARK_OPT_EINVAL, "d too large");
   if (((uintptr_t)embed_grad & 3u) || ((uintptr_t)dx0 & 3u) || ((uintptr_t)tokens & 3u))
     return fail(ARK_OPT_EINVAL, "embed_grad, dx0 or tokens not 4-byte aligned");

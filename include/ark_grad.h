@@ -51,7 +51,8 @@ int ark_grad_plan_destroy(ark_grad_plan *plan);
  * Every element receives its additions in increasing i, as in the loop: the
  * positions are stably sorted by token on the device, the dx0 rows copied in
  * that order, and each token's rows added in order, column by column.
- * embed_grad holds vocab*d floats, dx0 batch_seq*d, tokens batch_seq.
+ * embed_grad holds vocab*d floats, dx0 batch_seq*d, tokens batch_seq;
+ * batch_seq < 2^24 (one 256-lane block per token), d <= 65535 * 256.
  * Stream ordered; the scratch it needs (a copy of dx0, 16 B per token and
  * the sort's) comes from the stream-ordered pool. */
 int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,

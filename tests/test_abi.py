@@ -220,6 +220,10 @@ def test_next_rows_reject_bad_arguments_before_device_calls():
     assert (L.ark_grad_embed_scatter_noalloc(None, 0, 4, None, None, 3, None) == _abi.EINVAL
             and "vocab" in msg())
     assert L.ark_grad_embed_scatter_noalloc(None, 10, 4, None, None, 0, None) == 0
+    # one 256-lane block per token: 2^24 tokens would be 2^32 work-items
+    for f in (L.ark_grad_embed_scatter, L.ark_grad_embed_scatter_noalloc):
+        assert f(1 << 20, 10, 4, 2 << 20, 3 << 20, 1 << 24, None) == _abi.EINVAL
+        assert "too large" in msg(), msg()
     recs = (_abi.CkptRecord * 1)()
     recs[0] = _abi.CkptRecord(0, 4, 9, 0)
     out = C.c_uint64()
