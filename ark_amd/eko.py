@@ -66,8 +66,39 @@ EKO_237M = EkoConfig(n_layers=30, d_model=768, hidden=2048, vocab=32000)
 EKO_1P3B = EkoConfig(n_layers=24, d_model=2048, hidden=5504, vocab=32000, n_heads=16)
 
 
+SEGMENT = 4096  # ARK_OPT_NORM_SEGMENT: the optimizer cuts every tensor into these
+
+
+def shard_tensors(specs, rank, world):
+    """Rank `rank`'s share of `specs` when `world` GPUs split the optimizer's
+    segment list (every tensor cut into SEGMENT-element segments, in table
+    order) into contiguous runs of equal length to within one segment: the
+    tensors and tensor slices it owns, as 1-D TensorSpecs named
+    "name[lo:hi]" for a slice (ZeRO-1 style; w, g, m and v of a slice live
+    on its rank)."""
+    assert 0 <= rank < world
+    counts = [(s.n + SEGMENT - 1) // SEGMENT for s in specs]
+    total = sum(counts)
+    a, b = rank * total // world, (rank + 1) * total // world
+    out, s0 = [], 0
+    for spec, c in zip(specs, counts):
+        lo, hi = max(a, s0), min(b, s0 + c)
+        if lo < hi:
+            e0, e1 = (lo - s0) * SEGMENT, min(spec.n, (hi - s0) * SEGMENT)
+            if (e0, e1) == (0, spec.n):
+                out.append(spec)
+            else:
+                out.append(TensorSpec(f"{spec.name}[{e0}:{e1}]", (e1 - e0,), spec.decay,
+                                      spec.gain))
+        s0 += c
+    return out
+
+
 def config_tensors(name):
-    """TensorSpec list of a benchmark configuration: c0, c1, c2, c3, c4."""
+    """TensorSpec list of a benchmark configuration: c0, c1, c2, c3, c4, or
+    c2s8 / c4s8, rank 0's share of c2 / c4 over 8 GPUs (shard_tensors)."""
+    if name in ("c2s8", "c4s8"):
+        return shard_tensors(config_tensors(name[:2]), 0, 8)
     if name == "c0":
         return [TensorSpec("w", (768, 768), True, False)]
     if name == "c1":

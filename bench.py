@@ -46,6 +46,14 @@ WORKLOADS = {
                loss_scale=65536.0, sigma="loguniform"),
     "c4": dict(desc="1.3B scale-up: 24 layers, d 2048, ffn 5504, tied embed 32000x2048 (218 tensors)",
                loss_scale=65536.0, sigma=1e-3),
+    "c2s8": dict(desc="one GPU's share of c2 over 8 GPUs: rank 0's contiguous eighth of the "
+                      "segment list (tied embed, gamma_final, l0.wq..w1 and a slice of l0.w2); "
+                      "the step as that rank runs it, without the cross-GPU norm exchange",
+                 loss_scale=65536.0, sigma="loguniform"),
+    "c4s8": dict(desc="one GPU's share of c4 over 8 GPUs: rank 0's contiguous eighth of the "
+                      "segment list; the step as that rank runs it, without the cross-GPU "
+                      "norm exchange",
+                 loss_scale=65536.0, sigma=1e-3),
     "c1": dict(desc="one EKO layer (9 tensors)", loss_scale=1024.0, sigma=1e-3),
     "c0": dict(desc="single 768x768 tensor", loss_scale=1024.0, sigma=1e-3),
 }
