@@ -9,6 +9,8 @@ Mirrors (paths relative to proyecto_ark/ark01/ of the reference):
   Optimizer.record_overflow   src/training.rs:228-241
   Optimizer.restaurar_momentos  src/optimizer.rs:237-313
   ModelWeights / ParamSet       src/memory.rs:202-255 (device arenas)
+  adam_step_zero_copy   src/optimizer.rs:27-40 (one ark_asm_adam_step_f16 call)
+  adam_step             src/ffi.rs:98-101 (one ark_asm_adam_step call, fp32 w)
 
 Device memory and streams come from torch; every optimizer computation runs
 in the HIP library through its C ABI.
@@ -80,6 +82,41 @@ def lr_now(cfg: AdamConfig, step: int) -> float:
     cosine = f32(0.5) * (f32(1.0) + cos_f32(f32(np.pi) * progress))
     lr_min = lr * f32(0.1)
     return float(lr_min + (lr - lr_min) * cosine)
+
+
+def _single_tensor_args(w, g, m, v, w_bytes):
+    import torch
+    ts = (w, g, m, v)
+    if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() for t in ts):
+        raise ValueError("w, g, m and v must be contiguous device tensors")
+    if w_bytes == 4 and w.dtype != torch.float32:
+        raise ValueError("w must hold float32 elements")
+    if w_bytes == 2 and (w.element_size() != 2 or w.dtype == torch.bfloat16):
+        raise ValueError("w must hold float16 elements (or their bits as 16-bit integers)")
+    if not all(t.dtype == torch.float32 for t in (g, m, v)):
+        raise ValueError("g, m and v must be float32")
+    # optimizer.rs:32-33 (debug_assert_eq on the lengths)
+    if not (w.numel() == g.numel() == m.numel() == v.numel()):
+        raise ValueError(f"lengths differ: w {w.numel()}, g {g.numel()}, m {m.numel()}, "
+                         f"v {v.numel()}")
+    return (w.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), g.numel(),
+            C.c_void_p(torch.cuda.current_stream(w.device).cuda_stream))
+
+
+def adam_step_zero_copy(w_fp16, g, m, v, lr, beta1, beta2, eps, wd, t):
+    """optimizer.rs:27-40: AdamW over one tensor, fp16 weights (or their
+    16-bit bits) updated in place from fp32 g, m, v (ark_hip_adam_step_f16,
+    the drop-in of ark_asm_adam_step_f16, opti.s:192-360), queued on torch's
+    current stream of w's device."""
+    wp, gp, mp, vp, n, st = _single_tensor_args(w_fp16, g, m, v, 2)
+    check(lib().ark_hip_adam_step_f16(wp, gp, mp, vp, n, lr, beta1, beta2, eps, wd, t, st))
+
+
+def adam_step(w, g, m, v, lr, beta1, beta2, eps, wd, t):
+    """ffi.rs:98-101: the same over fp32 weights (ark_hip_adam_step, the
+    drop-in of ark_asm_adam_step, opti.s:20-177)."""
+    wp, gp, mp, vp, n, st = _single_tensor_args(w, g, m, v, 4)
+    check(lib().ark_hip_adam_step(wp, gp, mp, vp, n, lr, beta1, beta2, eps, wd, t, st))
 
 
 class ParamSet:

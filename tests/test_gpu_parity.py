@@ -378,6 +378,45 @@ def test_fp32_weight_dropin_matches_reference_kernel(n, off):
     assert np.array_equal(dw.cpu().numpy()[:off], w[:off])
 
 
+def test_python_wrappers_of_the_single_tensor_dropins():
+    """ark_amd.optimizer.adam_step_zero_copy (optimizer.rs:27-40) and
+    adam_step (ffi.rs:98-101) on torch's current stream, against the
+    oracle; length and dtype mismatches raise before any device call."""
+    torch = _torch()
+    from ark_amd.optimizer import adam_step, adam_step_zero_copy
+    rng = np.random.default_rng(11)
+    n = 70001
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-4).astype(np.float32)
+    v = (rng.random(n) * 1e-6).astype(np.float32)
+    w16 = oracle.synth_normal_f16(n, 5, 0, 0, 0.02)
+    w32 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dw16 = torch.from_numpy(w16.view(np.int16)).cuda().view(torch.float16)
+        dw32 = torch.from_numpy(w32).cuda()
+        dg = torch.from_numpy(g).cuda()
+        dm16, dv16, dm32, dv32 = (torch.from_numpy(a.copy()).cuda() for a in (m, v, m, v))
+        adam_step_zero_copy(dw16, dg, dm16, dv16, 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+        adam_step(dw32, dg, dm32, dv32, 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+    s.synchronize()
+    h = [a.copy() for a in (w16, m, v)]
+    oracle.adam_step_f16(h[0], g.copy(), h[1], h[2], 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+    assert not np.any(H.bits_differ16(dw16.cpu().view(torch.int16).numpy().view(np.uint16), h[0]))
+    assert not np.any(H.bits_differ32(dm16.cpu().numpy(), h[1]))
+    assert not np.any(H.bits_differ32(dv16.cpu().numpy(), h[2]))
+    h = [a.copy() for a in (w32, m, v)]
+    oracle.adam_step_f32(h[0], g.copy(), h[1], h[2], 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+    for d, e in zip((dw32, dm32, dv32), h):
+        assert not np.any(H.bits_differ32(d.cpu().numpy(), e))
+    with pytest.raises(ValueError, match="lengths differ"):
+        adam_step(dw32[1:], dg, dm32, dv32, 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+    with pytest.raises(ValueError, match="float32"):
+        adam_step(dw16, dg, dm32, dv32, 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+    with pytest.raises(ValueError, match="float16"):
+        adam_step_zero_copy(dw32, dg, dm32, dv32, 3e-4, 0.9, 0.95, 1e-8, 0.1, 4)
+
+
 def test_fp32_weight_dropin_special_values():
     """Subnormal, huge, infinite and NaN gradients and weights, zero moments
     and eps = 0 (0/0 -> NaN), through both the 16-byte and the per-element
