@@ -1,12 +1,26 @@
-"""Randomised GPU parity of the optimizer step: seeded random tensor tables
-(sizes from 1 element to several segments, exact multiples of the 4096
-segment and the 256-element row, element offsets that break 16-byte
-alignment), fp16 or fp32 gradients, the no-unscale flag, random
-hyperparameters, loss scales and clip thresholds, and occasional inf/NaN
-gradients; three steps each, every scalar and every w/m/v bit against the
-CPU oracle."""
-import ctypes as C
+"""Randomised GPU parity of the optimizer step (ark_opt_step) against the
+CPU oracle, bit for bit, on tables and hyperparameters no fixed
+configuration covers together.
 
+Each of 60 cases draws, from its own seed:
+  * 1-9 tensors with sizes from empty and single elements through exact
+    multiples of the 256-element row and the 4096-element segment and
+    ragged segment counts to ~40k elements, each at its own element offset
+    (0-7) in separate allocations, so 16-byte alignment breaks;
+  * per-tensor weight decay and the NO_UNSCALE flag (the gamma_final quirk);
+  * fp16 (loss-scaled) or fp32 gradients;
+  * beta1, beta2 (fixed and continuous values, 0 included), eps (0
+    included), grad_clip (tiny to never), the initial loss scale,
+    scale_up_every and the early-stop limit;
+  * starting m (signed) and v (non-negative), fp16 weights with some
+    subnormals and some gains of 1.0;
+and runs five steps with fresh gradients and a fresh lr each; gradient
+scales reach fp16 overflow (inf: a skipped step), and an inf, -inf or NaN is
+sometimes planted.  Every step's status and scalars and every w/m/v element
+are compared (optimizer.rs:126-228, training.rs:289-326, opti.s:192-360).
+A CPU test replays every case through the oracle alone and checks that the
+sweep reaches each of those outcomes.  A last test steps 3001 tensors, most
+of them tiny."""
 import numpy as np
 import pytest
 
@@ -14,9 +28,7 @@ import oracle
 from oracle import harness as H
 from ark_amd import _abi
 
-pytestmark = pytest.mark.gpu
-
-SIZES = [1, 3, 255, 256, 257, 1000, 4095, 4096, 4097, 8192, 12345, 3 * 4096 + 256]
+SIZES = [0, 1, 3, 255, 256, 257, 1000, 4095, 4096, 4097, 8192, 12345, 3 * 4096 + 256, 40000]
 
 
 def _torch():
@@ -25,92 +37,160 @@ def _torch():
     return torch
 
 
-def _bits16(t):
-    torch = _torch()
-    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+def _f16_bits(rng, n, sigma):
+    x = (rng.standard_normal(n) * sigma).astype(np.float16)
+    return x.view(np.uint16).copy()
 
 
-def _bits32(t):
-    torch = _torch()
-    return t.view(torch.int32).cpu().numpy().view(np.uint32)
+def _draw_grads(rng, n, grad_dtype, scale):
+    sigma = 10.0 ** rng.uniform(-7, -1) * scale
+    if rng.random() < 0.15:
+        sigma = 10.0 ** rng.uniform(3, 6)  # reaches fp16's range: inf, a skipped step
+    if grad_dtype == _abi.GRAD_F16:
+        with np.errstate(over="ignore"):
+            g = _f16_bits(rng, n, sigma)
+    else:
+        g = (rng.standard_normal(n) * sigma).astype(np.float32)
+    if n and rng.random() < 0.08:
+        bad = np.array([rng.choice([np.inf, -np.inf, np.nan])], np.float32)
+        g[int(rng.integers(n))] = (bad.astype(np.float16).view(np.uint16)[0]
+                                   if grad_dtype == _abi.GRAD_F16 else bad[0])
+    return g
 
 
-@pytest.mark.parametrize("case", range(60))
-def test_random_tables_match_oracle(case):
-    torch = _torch()
-    from ark_amd._lib import check, lib
+CASES = 60
+
+
+def draw_case(case):
+    """The case's hyperparameters, tensors (host arrays and element offsets)
+    and its per-step gradients and lrs, all from the case's seed."""
+    from ark_amd.optimizer import AdamConfig, AmpConfig
     rng = np.random.default_rng(1000 + case)
-    gdt = _abi.GRAD_F16 if case % 3 else _abi.GRAD_F32
-    nt = int(rng.integers(1, 9))
-    sizes = [int(rng.choice(SIZES)) if rng.random() < 0.7 else int(rng.integers(1, 30000))
-             for _ in range(nt)]
-    scale = float(2.0 ** rng.integers(0, 17))
-    hp = oracle.default_hparams()
-    hp.beta1 = float(np.float32(rng.choice([0.0, 0.5, 0.9, 0.99])))
-    hp.beta2 = float(np.float32(rng.choice([0.0, 0.95, 0.999])))
-    hp.eps = float(np.float32(rng.choice([1e-8, 1e-6, 1e-3])))
-    hp.grad_clip = float(np.float32(rng.choice([0.05, 1.0, 1e30])))
-    hp.loss_scale_init = scale
-    hp.loss_scale_max = 2.0 ** 24
-    hp.scale_up_every = int(rng.integers(1, 4))
-    hp.grad_dtype = gdt
-    lr = float(np.float32(rng.choice([1e-4, 3e-4, 1e-2])))
-
-    gnp = np.float16 if gdt == _abi.GRAD_F16 else np.float32
-    gtorch = torch.float16 if gdt == _abi.GRAD_F16 else torch.float32
-    dev, host, keep = [], [], []
-    for i, n in enumerate(sizes):
-        off = int(rng.integers(0, 8))  # elements: breaks 16-byte alignment for off % 8 != 0
-        w = (rng.standard_normal(n) * 0.05).astype(np.float16).view(np.uint16)
+    grad_dtype = _abi.GRAD_F16 if case % 3 else _abi.GRAD_F32
+    ntens = int(rng.integers(1, 10))
+    scale = float(2.0 ** int(rng.integers(0, 17)))
+    cfg = AdamConfig(lr=3e-4,
+                     beta1=float(np.float32(rng.choice([0.0, 0.5, 0.9, rng.uniform(0, 0.999)]))),
+                     beta2=float(np.float32(rng.choice([0.0, 0.95, 0.999,
+                                                        rng.uniform(0.5, 0.99999)]))),
+                     eps=float(rng.choice([0.0, 1e-8, 1e-6, 1e-3])),
+                     weight_decay=0.0,
+                     grad_clip=float(rng.choice([1e-3, 0.5, 1.0, 10.0, 1e30])))
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_max=2.0 ** 24,
+                    scale_up_every=int(rng.choice([1, 2, 3, 2000])),
+                    max_consecutive_nonfinite=int(rng.choice([1, 2, 200])))
+    tensors = []
+    for _ in range(ntens):
+        n = int(rng.choice(SIZES)) if rng.random() < 0.7 else int(rng.integers(1, 30000))
+        off = int(rng.integers(0, 8))
+        wd = float(np.float32(rng.choice([0.0, 0.01, 0.1, rng.uniform(0, 0.5)])))
+        flags = _abi.TENSOR_NO_UNSCALE if rng.random() < 0.2 else 0
+        w = _f16_bits(rng, n, 0.05)
+        if n and rng.random() < 0.3:  # some subnormal weights
+            k = max(1, n // 50)
+            w[rng.integers(n, size=k)] = rng.integers(1, 0x400, size=k)
+        if rng.random() < 0.15:
+            w[:] = 0x3C00  # a gain, initialised to 1.0
         m = (rng.standard_normal(n) * 1e-3).astype(np.float32)
-        v = np.abs(rng.standard_normal(n) * 1e-6).astype(np.float32)
-        wd = float(np.float32(rng.choice([0.0, 0.01, 0.1])))
-        flags = _abi.TENSOR_NO_UNSCALE if rng.random() < 0.15 else 0
-        bw = torch.zeros(n + off, dtype=torch.float16, device="cuda")
-        bg = torch.zeros(n + off, dtype=gtorch, device="cuda")
-        bm = torch.zeros(n + off, dtype=torch.float32, device="cuda")
-        bv = torch.zeros(n + off, dtype=torch.float32, device="cuda")
-        tw, tg, tm, tv = bw[off:], bg[off:], bm[off:], bv[off:]
-        tw.copy_(torch.from_numpy(w.view(np.int16)).view(torch.float16))
-        tm.copy_(torch.from_numpy(m))
-        tv.copy_(torch.from_numpy(v))
-        keep += [bw, bg, bm, bv]
-        dev.append((tw, tg, tm, tv, wd, flags))
-        host.append(oracle.HostTensor(w.copy(), np.zeros(n, np.uint16 if gdt == _abi.GRAD_F16
-                                                         else np.float32),
-                                      m.copy(), v.copy(), wd, flags))
-    tab = (_abi.Tensor * nt)()
-    for i, (tw, tg, tm, tv, wd, flags) in enumerate(dev):
-        tab[i] = _abi.Tensor(tw.data_ptr(), tg.data_ptr(), tm.data_ptr(), tv.data_ptr(),
-                             tw.numel(), wd, flags)
-    h = C.c_void_p()
-    check(lib().ark_opt_create(tab, nt, C.byref(hp), C.c_void_p(torch.cuda.current_stream()
-                                                                   .cuda_stream), C.byref(h)))
-    ref = oracle.Optimizer(host, hp)
-    try:
-        for k in range(3):
-            for i, n in enumerate(sizes):
-                sig = float(10.0 ** rng.uniform(-5, -1))
-                g = (rng.standard_normal(n) * sig * scale).astype(gnp)
-                if rng.random() < 0.08:
-                    g[int(rng.integers(0, n))] = rng.choice([np.inf, -np.inf, np.nan])
-                dev[i][1].copy_(torch.from_numpy(g))
-                host[i].g[:] = g.view(host[i].g.dtype)
-            gi = _abi.StepInfo()
-            rc = lib().ark_opt_step(h, lr, C.byref(gi))
-            rrc, ri = ref.step(lr)
-            assert rc == rrc, (k, rc, rrc)
-            d = H.info_matches(gi, ri)
-            assert not d, f"step {k}: {d}"
-            for i in range(nt):
-                tw, tg, tm, tv = dev[i][:4]
-                assert not np.any(H.bits_differ16(_bits16(tw), host[i].w)), (k, i, "w")
-                assert not np.any(H.bits_differ32(_bits32(tm).view(np.float32), host[i].m)), (k, i, "m")
-                assert not np.any(H.bits_differ32(_bits32(tv).view(np.float32), host[i].v)), (k, i, "v")
-    finally:
-        lib().ark_opt_destroy(h)
+        v = (np.abs(rng.standard_normal(n)) * 1e-6).astype(np.float32)
+        tensors.append(dict(n=n, off=off, wd=wd, flags=flags, w=w, m=m, v=v))
+    steps = []
+    for _ in range(5):
+        grads = [_draw_grads(rng, t["n"], grad_dtype, scale) for t in tensors]
+        steps.append((grads, float(np.float32(10.0 ** rng.uniform(-6, -2)))))
+    return grad_dtype, cfg, amp, tensors, steps
 
 
+def _host_tensors(tensors, steps):
+    return [oracle.HostTensor(t["w"].copy(), steps[0][0][i].copy(), t["m"].copy(),
+                              t["v"].copy(), t["wd"], t["flags"])
+            for i, t in enumerate(tensors)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(CASES))
+def test_random_tables_and_hyperparameters(case):
+    torch = _torch()
+    from ark_amd.optimizer import Optimizer
+    grad_dtype, cfg, amp, tensors, steps = draw_case(case)
+    gdt = torch.int16 if grad_dtype == _abi.GRAD_F16 else torch.float32
+    as_torch = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a)
+    bufs, arr = [], (_abi.Tensor * len(tensors))()
+    for i, t in enumerate(tensors):
+        n, off = t["n"], t["off"]
+        # each array in its own allocation, the tensor at element offset off
+        dw = torch.zeros(n + off + 8, dtype=torch.int16, device="cuda")
+        dg = torch.zeros(n + off + 8, dtype=gdt, device="cuda")
+        dm = torch.zeros(n + off + 8, dtype=torch.float32, device="cuda")
+        dv = torch.zeros(n + off + 8, dtype=torch.float32, device="cuda")
+        dw[off:off + n] = as_torch(t["w"])
+        dg[off:off + n] = as_torch(steps[0][0][i])
+        dm[off:off + n] = as_torch(t["m"])
+        dv[off:off + n] = as_torch(t["v"])
+        bufs.append((dw, dg, dm, dv, off, n))
+        arr[i].w, arr[i].g = dw.data_ptr() + 2 * off, dg.data_ptr() + dg.element_size() * off
+        arr[i].m, arr[i].v = dm.data_ptr() + 4 * off, dv.data_ptr() + 4 * off
+        arr[i].n, arr[i].weight_decay, arr[i].flags = n, t["wd"], t["flags"]
+    hosts = _host_tensors(tensors, steps)
+    torch.cuda.synchronize()
+    opt = Optimizer(cfg, _GradDtype(grad_dtype), amp, table=arr)
+    ref = oracle.Optimizer(hosts, opt.hp)
+    for k, (grads, lr) in enumerate(steps):
+        if k:
+            for (dw, dg, dm, dv, off, n), t, g in zip(bufs, hosts, grads):
+                t.g[:] = g
+                dg[off:off + n] = as_torch(g)
+        rc, gi = opt.step_all(lr, info=True)
+        rrc, ri = ref.step(lr)
+        assert rc == rrc, (case, k, rc, rrc)
+        d = H.info_matches(gi, ri)
+        assert not d, (case, k, d)
+        for i, ((dw, dg, dm, dv, off, n), t) in enumerate(zip(bufs, hosts)):
+            gw = dw[off:off + n].cpu().numpy().view(np.uint16)
+            assert not np.any(H.bits_differ16(gw, t.w)), (case, k, i, "w")
+            assert not np.any(H.bits_differ32(dm[off:off + n].cpu().numpy(), t.m)), (case, k, i)
+            assert not np.any(H.bits_differ32(dv[off:off + n].cpu().numpy(), t.v)), (case, k, i)
+    opt.close()
+
+
+def test_the_sweep_reaches_every_outcome():
+    """On the CPU, through the oracle alone: the cases' steps include
+    applied steps that clip and that do not, skipped steps, an early stop,
+    growth of the loss scale, both gradient types, unaligned tensors, empty
+    tensors and NO_UNSCALE tensors, so the GPU sweep compares all of them."""
+    from ark_amd.optimizer import hparams
+    seen = set()
+    for case in range(CASES):
+        grad_dtype, cfg, amp, tensors, steps = draw_case(case)
+        hosts = _host_tensors(tensors, steps)
+        ref = oracle.Optimizer(hosts, hparams(cfg, amp, grad_dtype))
+        scale0 = amp.loss_scale_init
+        for k, (grads, lr) in enumerate(steps):
+            for t, g in zip(hosts, grads):
+                t.g[:] = g
+            rc, info = ref.step(lr)
+            if rc == _abi.EARLY_STOP:
+                seen.add("early stop")
+            elif info.applied:
+                seen.add("clipped" if info.clipped else "unclipped")
+            else:
+                seen.add("skipped")
+            if info.state.loss_scale > scale0:
+                seen.add("growth")
+        seen.add(f"grad {grad_dtype}")
+        for t in tensors:
+            if t["off"]:
+                seen.add("unaligned")
+            if t["n"] == 0:
+                seen.add("empty")
+            if t["flags"]:
+                seen.add("no unscale")
+    want = {"clipped", "unclipped", "skipped", "early stop", "growth", "unaligned", "empty",
+            "no unscale", f"grad {_abi.GRAD_F16}", f"grad {_abi.GRAD_F32}"}
+    assert want <= seen, want - seen
+
+
+@pytest.mark.gpu
 def test_thousands_of_tiny_tensors():
     """3000 tensors of 1-300 elements: every segment ragged, every norm block
     mixed, a 3000-entry descriptor table; plus one tensor past a segment
@@ -138,3 +218,10 @@ def test_thousands_of_tiny_tensors():
     c = H.compare(ps, ts)
     assert c["w"] == c["m"] == c["v"] == 0, c
     opt.close()
+
+
+class _GradDtype:
+    """Stands in for a ParamSet where only the gradient dtype is read."""
+
+    def __init__(self, grad_dtype):
+        self.grad_dtype = grad_dtype
