@@ -657,12 +657,17 @@ __global__ __launch_bounds__(64) void adamw_single_w32_kernel(
 }  // namespace
 
 int sumsq_spb(uint64_t nseg) {
-  // 8 segments per block measured fastest for the norm pass (16 and 32 cost
-  // 10-50 % more); larger blocks only when the partials would exceed
-  // kMaxParts (beyond 2^31 elements).  A small table gets smaller blocks
-  // until the grid has two blocks per CU (512): the pass is then latency
-  // bound, and one EKO 768x768 tensor steps in 9.9 instead of 12.0 us.
-  int spb = 8;
+  // 2 segments (16 KiB of fp16 gradients) per block measured fastest for the
+  // norm pass on MI355X, fold included: 78.9 against 80.8 us at EKO-237M with
+  // 8, 15.1 against 18.0 us on an eighth of it, 55.7 against 57.3 us on an
+  // eighth of the 1.3B set; 1 segment per block is slower (93 us at
+  // EKO-237M: each block's descriptor load then stands alone in front of
+  // its data loads), as are 16 and 32.  Larger blocks only when the
+  // partials would exceed kMaxParts (beyond 2^30 elements).  A small table
+  // gets smaller blocks until the grid has two blocks per CU (512): the pass
+  // is then latency bound, and one EKO 768x768 tensor steps in 9.9 instead
+  // of 12.0 us.
+  int spb = 2;
   while (spb < 64 && (nseg + spb - 1) / spb > kMaxParts) spb *= 2;
   while (spb > 1 && (nseg + spb - 1) / spb < 512) spb /= 2;
   return spb;

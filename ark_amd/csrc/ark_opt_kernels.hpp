@@ -96,10 +96,12 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
-// Segments per sumsq block: 8; 16, 32 or 64 only past kMaxParts partials;
-// 4, 2 or 1 while fewer than 512 blocks would cover the table.
+// Segments per sumsq block: 2; 4 to 64 only past kMaxParts partials; 1
+// while fewer than 512 blocks would cover the table.
 int sumsq_spb(uint64_t nseg);
-constexpr uint32_t kMaxParts = 64u * kFinThreads;  // partial-buffer capacity
+// Partial-buffer capacity: past kFinTarget the partials are folded by
+// kFoldGroup, so the finalize reads at most kMaxParts / kFoldGroup = 4096.
+constexpr uint32_t kMaxParts = 256u * kFinThreads;
 // Above kFinTarget partials, fold_kernel first reduces aligned groups of
 // kFoldGroup (one wave each) so the finalize reads at most kFinTarget values.
 constexpr uint32_t kFinTarget = 8u * kFinThreads;
