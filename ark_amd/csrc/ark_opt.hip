@@ -55,13 +55,12 @@ struct ark_opt_handle {
   ark_opt_hparams hp{};
   int32_t ntensors = 0;
   uint32_t nseg = 0;
-  int spb = 8;
+  int spb = 2;
   uint32_t norm_blocks = 0;
   uint32_t nt_from = 0;  // norm blocks from here up stream past the cache
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
-  uint32_t* d_block_fast = nullptr;  // one flag per sumsq block
   double* d_part_sum = nullptr;  // one partial per norm block, zero-padded
   double* d_fold = nullptr;      // fold output when there are many partials
   uint32_t padded_parts = 0;     // power of two >= parts when folding
@@ -202,11 +201,11 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   }
   const uint64_t nseg = segs.size();
   int spb = ark::sumsq_spb(nseg);
-  // ARK_OPT_SUMSQ_SPB=1|2|4|...|64 overrides the segments per norm block (a
+  // ARK_OPT_SUMSQ_SPB=1|2|4|8 overrides the segments per norm block (a
   // tuning knob; the canonical tree makes the result independent of it).
   if (const char* env = getenv("ARK_OPT_SUMSQ_SPB")) {
     const int v = atoi(env);
-    if (v >= 1 && v <= 64 && (v & (v - 1)) == 0 && (nseg + v - 1) / v <= ark::kMaxParts)
+    if (v >= 1 && v <= 8 && (v & (v - 1)) == 0 && (nseg + v - 1) / v <= ark::kMaxParts)
       spb = v;
   }
   const uint64_t parts = (nseg + spb - 1) / spb;
@@ -256,15 +255,10 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->norm_blocks = (uint32_t)parts;
   h->nt_from = ark::sumsq_nt_from(spb, gsz);
 
-  // One allocation: segments | block flags | partial sums | state | scalars | info
+  // One allocation: segments | partial sums | state | scalars | info | units
   size_t off = 0;
   const size_t o_seg = off;
   off = align_up(off + sizeof(SegDesc) * (size_t)(nseg ? nseg : 1), 256);
-  std::vector<uint32_t> block_fast((size_t)(parts ? parts : 1), 0u);
-  for (uint64_t b = 0; b < parts; ++b)
-    block_fast[(size_t)b] = ark::sumsq_block_fast(segs.data(), nseg, spb, b);
-  const size_t o_fast = off;
-  off = align_up(off + sizeof(uint32_t) * block_fast.size(), 256);
   // Partials: up to kFinTarget go straight to the finalize (kFinThreads *
   // leaves doubles, zero past the real ones); more are first folded in
   // aligned groups of kFoldGroup from a power-of-two zero-padded buffer.
@@ -303,7 +297,6 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   }
   char* base = (char*)h->dev_mem;
   h->d_segs = (SegDesc*)(base + o_seg);
-  h->d_block_fast = (uint32_t*)(base + o_fast);
   h->d_part_sum = (double*)(base + o_psum);
   h->d_fold = fold ? (double*)(base + o_fold) : nullptr;
   h->padded_parts = padded;
@@ -332,9 +325,6 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   StepScalars sc{};
   e = hipSuccess;
   if (nseg) e = hipMemcpy(h->d_segs, segs.data(), sizeof(SegDesc) * nseg, hipMemcpyHostToDevice);
-  if (e == hipSuccess)
-    e = hipMemcpy(h->d_block_fast, block_fast.data(), sizeof(uint32_t) * block_fast.size(),
-                  hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(h->d_part_sum, 0, psum_bytes);
   if (e == hipSuccess && fold) e = hipMemset(h->d_fold, 0, fold_bytes);
   if (e == hipSuccess) e = hipMemcpy(h->d_state, &st, sizeof(st), hipMemcpyHostToDevice);
@@ -387,8 +377,7 @@ int step_impl(ark_opt_handle* h, float lr, const float* lr_dev, ark_opt_step_inf
                                        h->d_part_sum, h->stream));
     } else {
       ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
-                                h->nseg, h->d_block_fast, h->d_state, h->d_part_sum,
-                                h->nt_from, h->stream));
+                                h->nseg, h->d_state, h->d_part_sum, h->nt_from, h->stream));
     }
     if (h->d_fold)
       ARK_HIP(ark::launch_fold(h->padded_parts, h->d_part_sum, h->d_fold, h->stream));

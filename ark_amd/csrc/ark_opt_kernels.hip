@@ -149,19 +149,19 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // ---- kernel 1: sum of squares + non-finite flag -----------------------------
 
-// One batch of kRed full, 16-byte aligned segments starting at s0 into
+// One batch of kRed full, 16-byte aligned segments (descriptors d) into
 // vals[0, 2*kRed): every lane issues the loads of kLoad segments before using
 // any.  NT: non-temporal loads.
 template <typename GT, int kRed, int kLoad, bool NT>
-__device__ __forceinline__ void fast_batch(const SegDesc* __restrict__ segs, uint32_t s0,
-                                           int tid, float inv, double* vals, uint32_t& bad) {
+__device__ __forceinline__ void fast_batch(const SegDesc (&dsc)[kRed], int tid, float inv,
+                                           double* vals, uint32_t& bad) {
 #pragma unroll
   for (int b = 0; b < kRed; b += kLoad) {
     typename GradIO<GT>::Raw8 raw[2 * kLoad];
     float inv_k[kLoad];
 #pragma unroll
     for (int k = 0; k < kLoad; ++k) {
-      const SegDesc& d = segs[s0 + b + k];
+      const SegDesc& d = dsc[b + k];
       inv_k[k] = (d.flags & kSegNoUnscale) ? 1.0f : inv;
       const GT* g = static_cast<const GT*>(d.g);
       raw[2 * k] = GradIO<GT>::template load8<NT>(g + tid * kVec);
@@ -176,31 +176,24 @@ __device__ __forceinline__ void fast_batch(const SegDesc* __restrict__ segs, uin
   }
 }
 
-// Block b covers segments [b*SPB, b*SPB + SPB) in batches of kRed = min(SPB, 8)
-// segments.  Each batch reduces to the pairwise tree of its 16 half-segment
-// sums (an aligned subtree of the global tree); the block writes the pairwise
-// tree of its SPB/8 batch sums, again an aligned subtree.  Larger SPB keeps
-// the partial count, and so the finalize, small on big parameter sets.
-// A block that saw an inf or NaN gradient writes NaN, so the global sum is
-// NaN exactly when some gradient is non-finite (training.rs:291).
+// Block b covers segments [b*SPB, b*SPB + SPB) (SPB <= 8) and writes the
+// pairwise tree of their 2*SPB half-segment sums: an aligned subtree of the
+// global tree.  A block that saw an inf or NaN gradient writes NaN, so the
+// global sum is NaN exactly when some gradient is non-finite (training.rs:291).
 // Blocks from nt_from up read with non-temporal loads: they run first, and
 // what they read would leave the Infinity Cache before the AdamW pass gets
 // there; the blocks below (the last ~256 MiB read, where AdamW starts) keep
 // cache-allocating loads.
 template <typename GT, int SPB>
 __global__ __launch_bounds__(kBlock) void sumsq_kernel(
-    const SegDesc* __restrict__ segs, uint32_t nseg,
-    const uint32_t* __restrict__ block_fast, const ark_opt_state* __restrict__ state,
+    const SegDesc* __restrict__ segs, uint32_t nseg, const ark_opt_state* __restrict__ state,
     double* __restrict__ part_sum, uint32_t nt_from) {
-  constexpr int kRed = SPB < 8 ? SPB : 8;  // segments per in-block reduction
-  constexpr int NB = SPB / kRed;           // reductions per block
-  constexpr int V = 2 * kRed;              // half-segment values per lane
-  static_assert((SPB & (SPB - 1)) == 0 && SPB % kRed == 0 && (NB & (NB - 1)) == 0,
-                "power-of-two batches");
+  static_assert(SPB >= 1 && SPB <= 8 && (SPB & (SPB - 1)) == 0, "1, 2, 4 or 8 segments");
+  constexpr int V = 2 * SPB;  // half-segment values per lane
   // segments whose loads are in flight together (register budget)
   constexpr int kLoadMax = sizeof(GT) == 2 ? 8 : 4;
-  constexpr int kLoad = kLoadMax < kRed ? kLoadMax : kRed;
-  __shared__ double lds[2][kBlock / 64][V];
+  constexpr int kLoad = kLoadMax < SPB ? kLoadMax : SPB;
+  __shared__ double lds[kBlock / 64][V];
 
   // Blocks run in reverse: the last block, which usually holds the ragged
   // tail of the table, starts first instead of trailing the grid.
@@ -208,84 +201,81 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const float inv = 1.0f / state->loss_scale;  // training.rs:244
-  // precomputed at create: all SPB segments exist, are full and 16-byte
-  // aligned (one scalar load instead of a chain of dependent checks)
-  const bool fast = block_fast[blk] != 0u;
-  uint32_t bad = 0;
-  double bsum[NB];
+  const uint32_t s0 = blk * SPB;
+  // The block's descriptors come first, with no other load in front of them:
+  // whether it takes the vector path (every segment present, full and
+  // 16-byte aligned) follows from them by scalar compares, so the data loads
+  // wait for one scalar round trip.  Every field is in registers before the
+  // first branch, so the loads go out together instead of the compiler
+  // sinking the pointers' past the checks.
+  asm volatile("" : "+s"(nt_from));
+  float loss_scale = state->loss_scale;
+  SegDesc dsc[SPB];
+#pragma unroll
+  for (int k = 0; k < SPB; ++k) dsc[k] = segs[s0 + k < nseg ? s0 + k : nseg - 1u];
+#pragma unroll
+  for (int k = 0; k < SPB; ++k)
+    asm volatile("" : "+s"(dsc[k].g), "+s"(dsc[k].n), "+s"(dsc[k].flags));
+  asm volatile("" : "+s"(loss_scale));
+  const float inv = 1.0f / loss_scale;  // training.rs:244
+  bool fast = s0 + SPB <= nseg;
+#pragma unroll
+  for (int k = 0; k < SPB; ++k)
+    fast = fast && dsc[k].n == (uint32_t)kSeg && (dsc[k].flags & kSegVec) != 0u;
 
+  uint32_t bad = 0;
+  double vals[V];
+  if (fast && blk >= nt_from) {
+    fast_batch<GT, SPB, kLoad, true>(dsc, tid, inv, vals, bad);
+  } else if (fast) {
+    fast_batch<GT, SPB, kLoad, false>(dsc, tid, inv, vals, bad);
+  } else {
+    // some segment ragged, unaligned or past the end: full aligned segments
+    // still take the vector loads, the rest go element by element
 #pragma unroll
-  for (int r = 0; r < NB; ++r) {
-    const uint32_t s0 = blk * SPB + r * kRed;
-    double vals[V];
-    if (fast && blk >= nt_from) {
-      fast_batch<GT, kRed, kLoad, true>(segs, s0, tid, inv, vals, bad);
-    } else if (fast) {
-      fast_batch<GT, kRed, kLoad, false>(segs, s0, tid, inv, vals, bad);
-    } else {
-      // a block with some ragged, unaligned or past-the-end segment: full
-      // aligned segments still take the vector loads, the rest go element
-      // by element
+    for (int k = 0; k < SPB; ++k) {
+      if (s0 + k >= nseg) {
+        vals[2 * k] = 0.0;
+        vals[2 * k + 1] = 0.0;
+        continue;
+      }
+      const SegDesc& d = dsc[k];
+      const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : inv;
+      const GT* g = static_cast<const GT*>(d.g);
+      if (d.n == (uint32_t)kSeg && (d.flags & kSegVec)) {
+        const typename GradIO<GT>::Raw8 r0 = GradIO<GT>::load8(g + tid * kVec);
+        const typename GradIO<GT>::Raw8 r1 = GradIO<GT>::load8(g + kHalfSeg + tid * kVec);
+        float f[kVec];
+        GradIO<GT>::unpack8(r0, f, bad);
+        vals[2 * k] = group_sum(f, inv_t);
+        GradIO<GT>::unpack8(r1, f, bad);
+        vals[2 * k + 1] = group_sum(f, inv_t);
+        continue;
+      }
 #pragma unroll
-      for (int k = 0; k < kRed; ++k) {
-        const uint32_t s = s0 + k;
-        if (s >= nseg) {
-          vals[2 * k] = 0.0;
-          vals[2 * k + 1] = 0.0;
-          continue;
-        }
-        const SegDesc d = segs[s];
-        const float inv_t = (d.flags & kSegNoUnscale) ? 1.0f : inv;
-        const GT* g = static_cast<const GT*>(d.g);
-        if (d.n == (uint32_t)kSeg && (d.flags & kSegVec)) {
-          const typename GradIO<GT>::Raw8 r0 = GradIO<GT>::load8(g + tid * kVec);
-          const typename GradIO<GT>::Raw8 r1 = GradIO<GT>::load8(g + kHalfSeg + tid * kVec);
-          float f[kVec];
-          GradIO<GT>::unpack8(r0, f, bad);
-          vals[2 * k] = group_sum(f, inv_t);
-          GradIO<GT>::unpack8(r1, f, bad);
-          vals[2 * k + 1] = group_sum(f, inv_t);
-          continue;
-        }
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t e0 = h * kHalfSeg + tid * kVec;
+        float f[kVec];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t e0 = h * kHalfSeg + tid * kVec;
-          float f[kVec];
-#pragma unroll
-          for (int j = 0; j < kVec; ++j)
-            f[j] = (e0 + j < d.n) ? GradIO<GT>::load1(g + e0 + j, bad) : 0.0f;
-          vals[2 * k + h] = group_sum(f, inv_t);
-        }
+        for (int j = 0; j < kVec; ++j)
+          f[j] = (e0 + j < d.n) ? GradIO<GT>::load1(g + e0 + j, bad) : 0.0f;
+        vals[2 * k + h] = group_sum(f, inv_t);
       }
     }
-
-    int idx = 0;
-    transpose_reduce<V, 0>(vals, lane, idx);
-    const double wsum = butterfly_from<log2i(V)>(vals[0]);
-    // two LDS buffers: batch r+1 writes the other one while wave 0 reads
-    // this one; the barrier of batch r+1 orders the reuse of this one
-    if (lane < V) lds[r & 1][wave][idx] = wsum;
-    __syncthreads();
-    double x = 0.0;
-    if (wave == 0) {
-      if (lane < V)
-        x = (lds[r & 1][0][lane] + lds[r & 1][1][lane]) +
-            (lds[r & 1][2][lane] + lds[r & 1][3][lane]);
-      // pairwise over the V half-segment sums in lane (= index) order
-#pragma unroll
-      for (int s = 0; s < log2i(V); ++s) x = x + __shfl_xor(x, 1 << s);
-    }
-    bsum[r] = x;
   }
+
+  int idx = 0;
+  transpose_reduce<V, 0>(vals, lane, idx);
+  const double wsum = butterfly_from<log2i(V)>(vals[0]);
+  if (lane < V) lds[wave][idx] = wsum;
   const int any_bad = __syncthreads_or((int)bad);
-  if (tid == 0) {
-    // pairwise over the batch sums in index order
+  if (wave == 0) {
+    double x = 0.0;
+    if (lane < V) x = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+    // pairwise over the V half-segment sums in lane (= index) order
 #pragma unroll
-    for (int w = NB / 2; w >= 1; w /= 2)
-#pragma unroll
-      for (int i = 0; i < w; ++i) bsum[i] = bsum[2 * i] + bsum[2 * i + 1];
-    part_sum[blk] = any_bad ? __builtin_nan("") : bsum[0];
+    for (int st = 0; st < log2i(V); ++st) x = x + __shfl_xor(x, 1 << st);
+    if (tid == 0) part_sum[blk] = any_bad ? __builtin_nan("") : x;
   }
 }
 
@@ -302,7 +292,7 @@ __global__ __launch_bounds__(64) void units_reduce_kernel(const double* __restri
                                                           const SegDesc* __restrict__ segs,
                                                           uint32_t nseg,
                                                           double* __restrict__ part_sum) {
-  constexpr int U = SPB * kUnitsPerSeg;     // 16 .. 1024 units per block
+  constexpr int U = SPB * kUnitsPerSeg;     // 16 .. 128 units per block
   constexpr int K = U >= 64 ? U / 64 : 1;   // units per lane
   constexpr int L = U >= 64 ? 64 : U;       // lanes holding units
   static_assert(K <= kUnitsPerSeg, "a lane's units lie in one segment");
@@ -663,12 +653,13 @@ int sumsq_spb(uint64_t nseg) {
   // eighth of the 1.3B set; 1 segment per block is slower (93 us at
   // EKO-237M: each block's descriptor load then stands alone in front of
   // its data loads), as are 16 and 32.  Larger blocks only when the
-  // partials would exceed kMaxParts (beyond 2^30 elements).  A small table
+  // partials would exceed kMaxParts (beyond 2^31 elements); 8 covers every
+  // table kMaxSegments allows.  A small table
   // gets smaller blocks until the grid has two blocks per CU (512): the pass
   // is then latency bound, and one EKO 768x768 tensor steps in 9.9 instead
   // of 12.0 us.
   int spb = 2;
-  while (spb < 64 && (nseg + spb - 1) / spb > kMaxParts) spb *= 2;
+  while (spb < 8 && (nseg + spb - 1) / spb > kMaxParts) spb *= 2;
   while (spb > 1 && (nseg + spb - 1) / spb < 512) spb /= 2;
   return spb;
 }
@@ -682,28 +673,21 @@ hipError_t launch_fold(uint32_t padded_parts, const double* in, double* out,
 }
 
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
-                        const SegDesc* segs, uint32_t nseg, const uint32_t* block_fast,
-                        const ark_opt_state* state, double* part_sum, uint32_t nt_from,
-                        hipStream_t stream) {
+                        const SegDesc* segs, uint32_t nseg, const ark_opt_state* state,
+                        double* part_sum, uint32_t nt_from, hipStream_t stream) {
   const dim3 grid(nblocks), block(kBlock);
 #define ARK_SUMSQ(GT, SPB)                                                        \
   hipLaunchKernelGGL((sumsq_kernel<GT, SPB>), grid, block, 0, stream, segs, nseg, \
-                     block_fast, state, part_sum, nt_from)
+                     state, part_sum, nt_from)
   switch (spb * 2 + (grad_dtype == ARK_OPT_GRAD_F16 ? 0 : 1)) {
     case 2: ARK_SUMSQ(uint16_t, 1); break;
     case 4: ARK_SUMSQ(uint16_t, 2); break;
     case 8: ARK_SUMSQ(uint16_t, 4); break;
     case 16: ARK_SUMSQ(uint16_t, 8); break;
-    case 32: ARK_SUMSQ(uint16_t, 16); break;
-    case 64: ARK_SUMSQ(uint16_t, 32); break;
-    case 128: ARK_SUMSQ(uint16_t, 64); break;
     case 3: ARK_SUMSQ(float, 1); break;
     case 5: ARK_SUMSQ(float, 2); break;
     case 9: ARK_SUMSQ(float, 4); break;
     case 17: ARK_SUMSQ(float, 8); break;
-    case 33: ARK_SUMSQ(float, 16); break;
-    case 65: ARK_SUMSQ(float, 32); break;
-    case 129: ARK_SUMSQ(float, 64); break;
     default: return hipErrorInvalidValue;
   }
 #undef ARK_SUMSQ
@@ -722,9 +706,6 @@ hipError_t launch_units_reduce(int spb, uint32_t nblocks, const double* units,
     case 2: ARK_UNITS(2); break;
     case 4: ARK_UNITS(4); break;
     case 8: ARK_UNITS(8); break;
-    case 16: ARK_UNITS(16); break;
-    case 32: ARK_UNITS(32); break;
-    case 64: ARK_UNITS(64); break;
     default: return hipErrorInvalidValue;
   }
 #undef ARK_UNITS

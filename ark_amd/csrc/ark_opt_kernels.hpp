@@ -96,12 +96,12 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
-// Segments per sumsq block: 2; 4 to 64 only past kMaxParts partials; 1
+// Segments per sumsq block: 2; 4 or 8 only past kMaxParts partials; 1
 // while fewer than 512 blocks would cover the table.
 int sumsq_spb(uint64_t nseg);
 // Partial-buffer capacity: past kFinTarget the partials are folded by
-// kFoldGroup, so the finalize reads at most kMaxParts / kFoldGroup = 4096.
-constexpr uint32_t kMaxParts = 256u * kFinThreads;
+// kFoldGroup, so the finalize reads at most kMaxParts / kFoldGroup = 8192.
+constexpr uint32_t kMaxParts = 512u * kFinThreads;
 // Above kFinTarget partials, fold_kernel first reduces aligned groups of
 // kFoldGroup (one wave each) so the finalize reads at most kFinTarget values.
 constexpr uint32_t kFinTarget = 8u * kFinThreads;
@@ -114,19 +114,20 @@ hipError_t launch_fold(uint32_t padded_parts, const double* in, double* out,
 // adamw grid: one wave per row, 16 rows per segment; the grid must stay
 // below 2^32 work-items.
 constexpr uint64_t kMaxSegments = (1ull << 32) / (64ull * kRowsPerSeg) - 1;
+static_assert((kMaxSegments + 7) / 8 <= kMaxParts, "8 segments per norm block cover every table");
+static_assert(kMaxParts / kFoldGroup <= kFinTarget, "one fold leaves the finalize kFinTarget");
 
 // ---------------------------------------------------------------------------
 // Launch helpers (ark_opt_kernels.hip); each returns hipSuccess or the error.
 // ---------------------------------------------------------------------------
 
 // part_sum: one partial per block (NaN when the block saw a non-finite
-// gradient).  block_fast[b] != 0 when block b's spb segments all exist, hold
-// kSeg elements and carry kSegVec (see sumsq_block_fast).  Blocks b >= nt_from
-// read with non-temporal loads (see sumsq_nt_from).
+// gradient).  A batch of segments whose segments all exist, hold kSeg
+// elements and carry kSegVec takes 16-byte loads.  Blocks b >= nt_from read
+// with non-temporal loads (see sumsq_nt_from).
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
-                        const SegDesc* segs, uint32_t nseg, const uint32_t* block_fast,
-                        const ark_opt_state* state, double* part_sum, uint32_t nt_from,
-                        hipStream_t stream);
+                        const SegDesc* segs, uint32_t nseg, const ark_opt_state* state,
+                        double* part_sum, uint32_t nt_from, hipStream_t stream);
 
 // The norm pass leaves the last kNormCachedBytes it reads (its lowest
 // blocks, where the AdamW pass starts) in the Infinity Cache and streams the
@@ -138,17 +139,6 @@ inline uint32_t sumsq_nt_from(int spb, uint64_t grad_bytes) {
   const uint64_t per_block = (uint64_t)spb * kSeg * grad_bytes;
   const uint64_t b = kNormCachedBytes / per_block;
   return b > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)b;
-}
-
-// Host-side computation of the block_fast flags for a descriptor list.
-inline uint32_t sumsq_block_fast(const SegDesc* segs, uint64_t nseg, int spb, uint64_t block) {
-  const uint64_t s0 = block * (uint64_t)spb;
-  if (s0 + (uint64_t)spb > nseg) return 0u;
-  for (int k = 0; k < spb; ++k) {
-    const SegDesc& d = segs[s0 + k];
-    if (d.n != (uint32_t)kSeg || !(d.flags & kSegVec)) return 0u;
-  }
-  return 1u;
 }
 
 // Leaves per finalize thread for nparts partials (a power of two <= 64); the

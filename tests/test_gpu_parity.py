@@ -109,15 +109,15 @@ def test_config1_layer_hundred_steps_bit_exact():
 
 @pytest.mark.parametrize("grad_dtype", [_abi.GRAD_F16, _abi.GRAD_F32])
 def test_norm_blocking_does_not_change_bits(grad_dtype, monkeypatch):
-    """1, 2, 4, 8, 16, 32 or 64 segments per norm block (with ragged and
-    unaligned tensors, so fast and element-wise blocks mix) give the same
-    bits: the sum follows the canonical tree whatever the blocking."""
+    """1, 2, 4 or 8 segments per norm block (with ragged and unaligned
+    tensors, so fast and element-wise blocks mix) give the same bits: the
+    sum follows the canonical tree whatever the blocking."""
     torch = _torch()
     specs = config_tensors("c1") + [TensorSpec("r", (4096 * 70 + 3,), True, False),
                                     TensorSpec("s", (5,), False, True)]
     sig = [1e-3] * len(specs)
     base = None
-    for spb in ("1", "2", "4", "8", "16", "32", "64"):
+    for spb in ("1", "2", "4", "8"):
         monkeypatch.setenv("ARK_OPT_SUMSQ_SPB", spb)
         cfg, ps, ts, opt, ref = _make(specs, 21, sig, 4096.0, grad_dtype=grad_dtype)
         _, gi = opt.step_all(cfg.lr, info=True)
