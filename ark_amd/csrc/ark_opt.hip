@@ -200,7 +200,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
     }
   }
   const uint64_t nseg = segs.size();
-  int spb = ark::sumsq_spb(nseg);
+  int spb = ark::sumsq_spb(nseg, hp->grad_dtype);
   // ARK_OPT_SUMSQ_SPB=1|2|4|8 overrides the segments per norm block (a
   // tuning knob; the canonical tree makes the result independent of it).
   if (const char* env = getenv("ARK_OPT_SUMSQ_SPB")) {

@@ -646,19 +646,24 @@ __global__ __launch_bounds__(64) void adamw_single_w32_kernel(
 
 }  // namespace
 
-int sumsq_spb(uint64_t nseg) {
-  // 2 segments (16 KiB of fp16 gradients) per block measured fastest for the
+int sumsq_spb(uint64_t nseg, uint32_t grad_dtype) {
+  // fp16 gradients: 2 segments (16 KiB) per block measured fastest for the
   // norm pass on MI355X, fold included: 78.9 against 80.8 us at EKO-237M with
   // 8, 15.1 against 18.0 us on an eighth of it, 55.7 against 57.3 us on an
   // eighth of the 1.3B set; 1 segment per block is slower (93 us at
   // EKO-237M: each block's descriptor load then stands alone in front of
-  // its data loads), as are 16 and 32.  Larger blocks only when the
-  // partials would exceed kMaxParts (beyond 2^31 elements); 8 covers every
-  // table kMaxSegments allows.  A small table
+  // its data loads), as are 16 and 32.
+  // fp32 gradients: 8.  Such a handle's norm usually comes from the units
+  // the gradient hand-off wrote (units_reduce_kernel: one wave per block
+  // reads 16 doubles per segment), whose cost is per block, not per byte: at
+  // EKO-237M 4.5 us with 8 segments per block and no fold, against 8.5 us
+  // plus a 4.5 us fold with 2 (the reading pass gains 4.6 us with 2).
+  // Larger blocks only when the partials would exceed kMaxParts (beyond
+  // 2^31 elements); 8 covers every table kMaxSegments allows.  A small table
   // gets smaller blocks until the grid has two blocks per CU (512): the pass
   // is then latency bound, and one EKO 768x768 tensor steps in 9.9 instead
   // of 12.0 us.
-  int spb = 2;
+  int spb = grad_dtype == ARK_OPT_GRAD_F32 ? 8 : 2;
   while (spb < 8 && (nseg + spb - 1) / spb > kMaxParts) spb *= 2;
   while (spb > 1 && (nseg + spb - 1) / spb < 512) spb /= 2;
   return spb;

@@ -96,9 +96,10 @@ __host__ __device__ inline float lr_eff_of(float lr, float beta1, float beta2,
   return r * lr;
 }
 
-// Segments per sumsq block: 2; 4 or 8 only past kMaxParts partials; 1
-// while fewer than 512 blocks would cover the table.
-int sumsq_spb(uint64_t nseg);
+// Segments per norm block: 2 for fp16 gradients, 8 for fp32 (4 or 8 past
+// kMaxParts partials); halved while fewer than 512 blocks would cover the
+// table.
+int sumsq_spb(uint64_t nseg, uint32_t grad_dtype);
 // Partial-buffer capacity: past kFinTarget the partials are folded by
 // kFoldGroup, so the finalize reads at most kMaxParts / kFoldGroup = 8192.
 constexpr uint32_t kMaxParts = 512u * kFinThreads;
