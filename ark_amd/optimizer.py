@@ -89,6 +89,8 @@ def _single_tensor_args(w, g, m, v, w_bytes):
     ts = (w, g, m, v)
     if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() for t in ts):
         raise ValueError("w, g, m and v must be contiguous device tensors")
+    if len({t.device for t in ts}) != 1:
+        raise ValueError("w, g, m and v must be on one device")
     if w_bytes == 4 and w.dtype != torch.float32:
         raise ValueError("w must hold float32 elements")
     if w_bytes == 2 and (w.element_size() != 2 or w.dtype == torch.bfloat16):
