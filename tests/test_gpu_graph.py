@@ -133,3 +133,69 @@ def test_a_non_finite_device_lr_leaves_everything_as_it_was():
     rc, info = o.step_lr_dev(lr_dev, info=True)
     assert rc == _abi.OK and info.applied == 1 and info.lr == pytest.approx(3e-4)
     o.close()
+
+
+def test_final_accumulation_and_step_captured_together():
+    """The gradient plan's final accumulation (which also writes the norm's
+    units) and the step on fp32 gradients captured in one graph, replayed
+    over fresh backward outputs with the lr rewritten in its device scalar
+    before each replay: every replay leaves the same w, m, v, gradient and
+    state bits as the same two calls made eagerly on an identical problem.
+    Capture records no host-side decision that a replay would get wrong:
+    the accumulation marks the units fresh and the captured step consumes
+    them, both inside the graph."""
+    torch = _torch()
+    from ark_amd import _abi, synth
+    from ark_amd.grad import GradPlan
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    specs = config_tensors("c1")
+    sig = [1e-3] * len(specs)
+    scale, seed = 256.0, 41
+    cfg = AdamConfig(lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0,
+                     warmup_steps=10)
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_max=2.0 ** 24)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        pa = H.gpu_problem(specs, seed, cfg.weight_decay, sig, scale, grad_dtype=_abi.GRAD_F32)
+        pb = H.gpu_problem(specs, seed, cfg.weight_decay, sig, scale, grad_dtype=_abi.GRAD_F32)
+        oa, ob = Optimizer(cfg, pa, amp, stream=s), Optimizer(cfg, pb, amp, stream=s)
+        outs_a = [torch.empty_like(pa.g(i)) for i in range(len(specs))]
+        outs_b = [torch.empty_like(pb.g(i)) for i in range(len(specs))]
+        plan_a = GradPlan(list(zip([pa.g(i) for i in range(len(specs))], outs_a)), stream=s)
+        plan_b = GradPlan(list(zip([pb.g(i) for i in range(len(specs))], outs_b)), stream=s)
+        lr_dev = torch.zeros(1, dtype=torch.float32, device="cuda")
+
+    def backward_outputs(k):
+        for i in range(len(specs)):
+            ss = synth.grad_sigma_scale(sig[i], scale)
+            synth.normal_f32(outs_a[i], seed + 7, i, k, ss)
+            synth.normal_f32(outs_b[i], seed + 7, i, k, ss)
+
+    with torch.cuda.stream(s):
+        backward_outputs(0)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        plan_a.run(final_for=oa)
+        oa.step_lr_dev(lr_dev)
+    # capture ran no kernel: both problems are still at step 0
+    assert oa.get_state().t == ob.get_state().t == 0
+    lrs = set()
+    for k in range(1, 7):
+        lr = ob.lr_now(k)
+        lrs.add(lr)
+        with torch.cuda.stream(s):
+            backward_outputs(k)
+            lr_dev.fill_(lr)
+            g.replay()
+            plan_b.run(final_for=ob)
+            ob.step_all(lr)
+        s.synchronize()
+        sa, sb = oa.get_state(), ob.get_state()
+        assert sa.as_dict() == sb.as_dict() and sa.t == k, (k, sa.as_dict(), sb.as_dict())
+        _same(pa, pb, len(specs), k)
+        for i in range(len(specs)):
+            assert torch.equal(pa.g(i).view(torch.int32), pb.g(i).view(torch.int32)), (k, i)
+    assert len(lrs) == 6  # the warmup changes lr on every replay
+    plan_a.close(), plan_b.close()
+    oa.close(), ob.close()
