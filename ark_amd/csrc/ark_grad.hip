@@ -643,6 +643,14 @@ int scatter_check(const float* embed_grad, uint32_t vocab, uint32_t d, const uin
   return ARK_OPT_OK;
 }
 
+// A scatter not made through the final call: any optimizer handle whose
+// norm units cover embed_grad loses them (its next step reads the gradients).
+void invalidate_embed_units(const float* embed_grad, uint32_t vocab, uint32_t d) {
+  const void* p = embed_grad;
+  const uint64_t b = (uint64_t)vocab * d * 4;
+  ark::opt_units_invalidate(&p, &b, 1);
+}
+
 // Queues the scatter on s with its workspace at ws (L.bytes bytes, 256-byte
 // aligned): the sort, the row copy and the run adds.
 int scatter_launch(float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t* tokens,
@@ -742,6 +750,7 @@ struct ark_grad_plan {
   GradSeg* d_segs = nullptr;
   std::vector<const float*> span_dst;  // the spans as given, for matching an
   std::vector<uint64_t> span_n;        // optimizer table
+  std::vector<uint64_t> span_bytes;    // 4 * span_n
 };
 
 extern "C" {
@@ -755,6 +764,11 @@ int ark_grad_accumulate(float* dst, const float* src, uint64_t n, void* stream) 
   if ((rc = ark::check_buffer(dst, n * 4, "dst", 0))) return rc;
   if ((rc = ark::check_buffer(src, n * 4, "src", 0))) return rc;
   if (overlaps(dst, n * 4, src, n * 4)) return fail(ARK_OPT_EINVAL, "dst and src overlap");
+  {
+    const void* d = dst;
+    const uint64_t b = n * 4;
+    ark::opt_units_invalidate(&d, &b, 1);
+  }
   const uint32_t vec = ((((uintptr_t)dst | (uintptr_t)src) & 15u) == 0) ? 1u : 0u;
   uint64_t blocks = ((n + kPerLane - 1) / kPerLane + kThreads - 1) / kThreads;
   if (blocks > kMaxFlatBlocks) blocks = kMaxFlatBlocks;
@@ -801,6 +815,7 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
   for (int32_t i = 0; i < n_spans; ++i) {
     p->span_dst.push_back(spans[i].dst);
     p->span_n.push_back(spans[i].n);
+    p->span_bytes.push_back(spans[i].n * 4u);
   }
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess && !segs.empty()) {
@@ -820,6 +835,8 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
 int ark_grad_plan_run(ark_grad_plan* p) {
   if (!p) return fail(ARK_OPT_EINVAL, "plan is NULL");
   if (p->nseg == 0) return ARK_OPT_OK;
+  ark::opt_units_invalidate(reinterpret_cast<const void* const*>(p->span_dst.data()),
+                            p->span_bytes.data(), p->span_dst.size());
   ark::DeviceGuard g(p->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
   hipLaunchKernelGGL(grad_batch, dim3(p->nseg * kBlocksPerSeg), dim3(kWave), 0, p->stream,
@@ -867,6 +884,7 @@ int ark_grad_embed_scatter(float* embed_grad, uint32_t vocab, uint32_t d, const 
   bool skip = false;
   int rc = scatter_check(embed_grad, vocab, d, tokens, dx0, batch_seq, &skip);
   if (rc || skip) return rc;
+  invalidate_embed_units(embed_grad, vocab, d);
   hipStream_t s = (hipStream_t)stream;
   const ScatterLayout L = scatter_layout(batch_seq, d);
   StreamBuf ws;
@@ -937,6 +955,7 @@ int ark_grad_embed_scatter_noalloc(float* embed_grad, uint32_t vocab, uint32_t d
   }
   void* ws = nullptr;
   if ((rc = scratch_ptr(dev, &ws))) return rc;
+  invalidate_embed_units(embed_grad, vocab, d);
   return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws, L, s);
 }
 

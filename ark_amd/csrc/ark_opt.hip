@@ -7,6 +7,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -90,6 +92,30 @@ struct ark_opt_handle {
 };
 
 namespace {
+
+// Handles whose units are fresh (written by the gradient hand-off's final
+// calls for their next step).  The library's other gradient writers look
+// here (ark::opt_units_invalidate) so that a write after the final calls
+// makes that step read the gradients instead of stale units.  Usually empty
+// or one handle.
+std::mutex g_fresh_mu;
+std::vector<ark_opt_handle*> g_fresh;
+
+void set_fresh_locked(ark_opt_handle* h, bool fresh) {
+  h->units_fresh = fresh;
+  auto it = std::find(g_fresh.begin(), g_fresh.end(), h);
+  if (fresh && it == g_fresh.end()) g_fresh.push_back(h);
+  if (!fresh && it != g_fresh.end()) g_fresh.erase(it);
+}
+
+// Whether h's units are fresh; either way they are not afterwards (a step
+// consumes them).
+bool take_fresh_units(ark_opt_handle* h) {
+  std::lock_guard<std::mutex> lock(g_fresh_mu);
+  const bool was = h->units_fresh;
+  set_fresh_locked(h, false);
+  return was;
+}
 
 int fold_timing(ark_opt_handle* h) {
   if (h->pending == 0) return ARK_OPT_OK;
@@ -339,6 +365,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
 int ark_opt_destroy(ark_opt_handle* h) {
   if (!h) return ARK_OPT_OK;
+  ark::opt_units_set_fresh(h, false);
   DeviceGuard g(h->device);
   (void)hipStreamSynchronize(h->stream);
   free_handle(h);
@@ -370,9 +397,8 @@ int step_impl(ark_opt_handle* h, float lr, const float* lr_dev, ark_opt_step_inf
     ARK_HIP(hipEventRecord(ev[0], h->stream));
   }
   if (h->nseg) {
-    if (h->units_fresh) {
+    if (take_fresh_units(h)) {
       // the gradients' producers already formed the tree's first level
-      h->units_fresh = false;
       ARK_HIP(ark::launch_units_reduce(h->spb, h->norm_blocks, h->d_units, h->d_segs, h->nseg,
                                        h->d_part_sum, h->stream));
     } else {
@@ -425,7 +451,7 @@ int ark_opt_record_overflow(ark_opt_handle* h, ark_opt_step_info* info) {
   if (!h) return fail(ARK_OPT_EINVAL, "handle is NULL");
   DeviceGuard g(h->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
-  h->units_fresh = false;  // the loss scale they were unscaled by changes
+  ark::opt_units_set_fresh(h, false);  // the loss scale they were unscaled by changes
   ARK_HIP(ark::launch_record_overflow(h->hp, h->d_state, h->d_info, h->stream));
   if (info) return finish_info(h, info);
   return ARK_OPT_OK;
@@ -449,7 +475,7 @@ int ark_opt_set_state(ark_opt_handle* h, const ark_opt_state* st) {
   DeviceGuard g(h->device);
   if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", h->device);
   ARK_HIP(hipStreamSynchronize(h->stream));
-  h->units_fresh = false;  // the loss scale they were unscaled by may change
+  ark::opt_units_set_fresh(h, false);  // the loss scale they were unscaled by may change
   *h->h_state = *st;
   ARK_HIP(hipMemcpyAsync(h->d_state, h->h_state, sizeof(ark_opt_state),
                          hipMemcpyHostToDevice, h->stream));
@@ -609,6 +635,30 @@ int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, bool requ
               g, (unsigned long long)n);
 }
 
-void opt_units_set_fresh(ark_opt_handle* h, bool fresh) { h->units_fresh = fresh; }
+void opt_units_set_fresh(ark_opt_handle* h, bool fresh) {
+  std::lock_guard<std::mutex> lock(g_fresh_mu);
+  set_fresh_locked(h, fresh);
+}
+
+void opt_units_invalidate(const void* const* dst, const uint64_t* bytes, size_t count) {
+  std::lock_guard<std::mutex> lock(g_fresh_mu);
+  for (size_t k = 0; k < g_fresh.size();) {
+    ark_opt_handle* h = g_fresh[k];
+    bool hit = false;
+    for (size_t i = 0; i < count && !hit; ++i) {
+      if (bytes[i] == 0) continue;
+      for (const ark_opt_handle::TensorInfo& t : h->tensors) {
+        if (t.n && overlaps(t.g, t.n * 4u, dst[i], bytes[i])) {
+          hit = true;
+          break;
+        }
+      }
+    }
+    if (hit)
+      set_fresh_locked(h, false);
+    else
+      ++k;
+  }
+}
 
 }  // namespace ark

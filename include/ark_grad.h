@@ -71,12 +71,14 @@ int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
  *   ark_grad_plan_run_final(plan, opt);              every grad += output
  *   ark_grad_embed_scatter_final(..., opt);          the token scatter
  *   ark_opt_step(opt, lr, info);
- * Between the final calls and the step the gradients must not change by
- * any other route (another accumulation, ark_grad_embed_scatter, a copy): the
- * step would use the units of the old values.  ark_opt_set_state and
- * ark_opt_record_overflow discard the units (the loss scale changes), as does
- * every ark_opt_step after using them; a step without fresh units reads the
- * gradients as usual. */
+ * Between the final calls and the step, a write to the handle's gradients
+ * through this library's other calls (ark_grad_accumulate,
+ * ark_grad_plan_run, ark_grad_embed_scatter, ark_grad_embed_scatter_noalloc)
+ * discards the units; a write the library does not see (the caller's own
+ * kernel or copy) must not happen: the step would use the units of the old
+ * values.  ark_opt_set_state and ark_opt_record_overflow discard the units
+ * (the loss scale changes), as does every ark_opt_step after using them; a
+ * step without fresh units reads the gradients as usual. */
 
 /* As ark_grad_plan_run, as the last accumulation before opt's next step:
  * also writes the norm's units of every span into opt.  opt must take fp32

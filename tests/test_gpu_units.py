@@ -178,6 +178,42 @@ def test_units_are_discarded_when_the_loss_scale_or_gradients_change():
     a.close(), b.close()
 
 
+@pytest.mark.parametrize("route", ["accumulate", "plan", "scatter", "scatter_noalloc"])
+def test_library_gradient_writes_after_the_final_calls_drop_the_units(route):
+    """After the final accumulation, a further write to a gradient through
+    the library's plain calls (ark_grad_accumulate, ark_grad_plan_run,
+    ark_grad_embed_scatter and its no-allocation form) makes the next step
+    read the gradients instead of the units the final call wrote: the step
+    equals, bit for bit, that of a twin problem that never had units."""
+    torch = _torch()
+    specs = EkoConfig(n_layers=1, d_model=256, hidden=512, vocab=100).tensors()
+    e = [s.name for s in specs].index("embed")
+    outs = _outs(specs, 6, 1e-3, 1024.0)
+    extra = _outs(specs, 7, 1e-2, 1024.0)
+    tokens = torch.tensor([3, 7, 3, 99, 150], dtype=torch.int32, device="cuda")
+    dx0 = torch.randn(5, 256, device="cuda", generator=torch.Generator(device="cuda")
+                      .manual_seed(8)) * 10.0
+    a, b = (_Run(specs, outs, 1024.0) for _ in range(2))
+    for r in (a, b):
+        for i in range(len(specs)):
+            r.ps.g(i).zero_()
+    a.plan.run(final_for=a.opt)  # a's units now describe these gradients
+    b.plan.run()
+    for r in (a, b):
+        if route == "accumulate":
+            grad.accumulate(r.ps.g(1), extra[1])
+        elif route == "plan":
+            r.plan.run()
+        else:
+            grad.embed_scatter(r.ps.g(e).view(100, 256), tokens, dx0,
+                               noalloc=(route == "scatter_noalloc"))
+    ia = a.opt.step_all(a.cfg.lr, info=True)[1]
+    ib = b.opt.step_all(b.cfg.lr, info=True)[1]
+    _info_eq(ia, ib)
+    _same(a, b, specs)
+    a.close(), b.close()
+
+
 def test_final_calls_refuse_mismatched_handles():
     torch = _torch()
     from ark_amd._lib import ArkOptError, lib
