@@ -69,6 +69,20 @@ constexpr int kUnpackUnits = 2;
 constexpr uint32_t unpack_seg(uint32_t ftype) {
   return (ftype == ARK_CKPT_F16 ? 8u : 4u) * kUnpackLanes * kUnpackUnits;
 }
+// blocks per launch of each, so that a launch's work-items stay below 2^32
+constexpr uint64_t kPackMaxBlocks = ((1ull << 32) - 1) / kPackLanes;
+constexpr uint64_t kUnpackMaxBlocks = ((1ull << 32) - 1) / kUnpackLanes;
+
+// ARK_CKPT_LAUNCH_BLOCKS=k (k >= 1) caps the blocks per pack or unpack launch
+// below that (a test knob: it splits even small images over many launches,
+// which must give the same bytes).
+uint64_t launch_blocks(uint64_t max_blocks) {
+  if (const char* env = getenv("ARK_CKPT_LAUNCH_BLOCKS")) {
+    const long long v = atoll(env);
+    if (v >= 1 && (uint64_t)v < max_blocks) return (uint64_t)v;
+  }
+  return max_blocks;
+}
 constexpr size_t kStageBytes = (size_t)64 << 20;      // per pinned staging buffer
 static_assert(sizeof(ark_opt_state) == 32, "trailer holds a 32-byte state");
 
@@ -168,12 +182,14 @@ __device__ __forceinline__ uint32_t find_rec(const uint32_t* __restrict__ start,
 __global__ __launch_bounds__(kPackLanes) void pack_kernel(const PackRec* __restrict__ recs,
                                                           const uint32_t* __restrict__ start,
                                                           const uint32_t* __restrict__ hint,
-                                                          uint8_t* __restrict__ img) {
-  const uint32_t r = find_rec(start, hint, blockIdx.x);
+                                                          uint8_t* __restrict__ img,
+                                                          uint32_t block0) {
+  const uint32_t blk = block0 + blockIdx.x;
+  const uint32_t r = find_rec(start, hint, blk);
   const PackRec s = recs[r];
   const uint64_t base = s.data_off & ~15ull;
   const uint64_t end = s.data_off + s.src_bytes;
-  const uint64_t c0 = base + (uint64_t)(blockIdx.x - start[r]) * kPackSegBytes;
+  const uint64_t c0 = base + (uint64_t)(blk - start[r]) * kPackSegBytes;
   const uint64_t seg_lo = c0 > s.data_off ? c0 : s.data_off;
   const uint64_t seg_hi = c0 + kPackSegBytes < end ? c0 + kPackSegBytes : end;
 #pragma unroll
@@ -308,10 +324,11 @@ __global__ __launch_bounds__(kUnpackLanes) void unpack_kernel(const UnpackRec* _
                                                             const uint32_t* __restrict__ start,
                                                             const uint32_t* __restrict__ hint,
                                                             const uint8_t* __restrict__ img,
-                                                            uint64_t img_bytes) {
-  const uint32_t r = find_rec(start, hint, blockIdx.x);
+                                                            uint64_t img_bytes, uint32_t block0) {
+  const uint32_t blk = block0 + blockIdx.x;
+  const uint32_t r = find_rec(start, hint, blk);
   const UnpackRec s = recs[r];
-  const uint64_t e_begin = (uint64_t)(blockIdx.x - start[r]) * unpack_seg(s.ftype);
+  const uint64_t e_begin = (uint64_t)(blk - start[r]) * unpack_seg(s.ftype);
   if (s.ftype == ARK_CKPT_F16)
     unpack_block<ARK_CKPT_F16>(s, e_begin, img, img_bytes);
   else
@@ -522,9 +539,12 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
   hipLaunchKernelGGL(header_kernel, dim3((np + kThreads - 1) / kThreads), dim3(kThreads), 0,
                      stream, dp, np, img);
   ARK_HIP(hipGetLastError());
-  if (blocks) {
-    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kPackLanes), 0, stream, dr, dst,
-                       dhint, img);
+  // a launch's work-items stay below 2^32: images past 64 GiB take several
+  const uint64_t per_launch = launch_blocks(kPackMaxBlocks);
+  for (uint64_t b0 = 0; b0 < blocks; b0 += per_launch) {
+    const uint64_t nb = blocks - b0 < per_launch ? blocks - b0 : per_launch;
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)nb), dim3(kPackLanes), 0, stream, dr, dst,
+                       dhint, img, (uint32_t)b0);
     ARK_HIP(hipGetLastError());
   }
   ARK_HIP(hipStreamSynchronize(stream));
@@ -570,10 +590,15 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
   }
   StreamSync sync{stream};
   ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
-  hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kUnpackLanes), 0, stream,
-                     (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb),
-                     (const uint32_t*)((char*)d.p + rb + stb), img, img_bytes);
-  ARK_HIP(hipGetLastError());
+  // a launch's work-items stay below 2^32: checkpoints past 128 GiB take several
+  const uint64_t per_launch = launch_blocks(kUnpackMaxBlocks);
+  for (uint64_t b0 = 0; b0 < blocks; b0 += per_launch) {
+    const uint64_t nb = blocks - b0 < per_launch ? blocks - b0 : per_launch;
+    hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)nb), dim3(kUnpackLanes), 0, stream,
+                       (const UnpackRec*)d.p, (const uint32_t*)((char*)d.p + rb),
+                       (const uint32_t*)((char*)d.p + rb + stb), img, img_bytes, (uint32_t)b0);
+    ARK_HIP(hipGetLastError());
+  }
   ARK_HIP(hipStreamSynchronize(stream));
   return ARK_OPT_OK;
 }

@@ -178,6 +178,33 @@ def test_full_eko237m_image():
             np.testing.assert_array_equal(_bits(b), _quiet16(_bits(a)))
 
 
+@pytest.mark.parametrize("per_launch", ["1", "7", "1000"])
+def test_pack_and_unpack_split_over_launches(per_launch, monkeypatch):
+    """Pack and unpack launch at most 2^32 work-items at a time, so an image
+    past 64 GiB (pack) or 128 GiB (unpack) takes several launches, each from
+    a block offset.  ARK_CKPT_LAUNCH_BLOCKS caps the blocks per launch so that
+    a small image takes that path too: the image is byte-identical to the
+    one-launch image, and unpacking it restores every buffer."""
+    torch = _torch()
+    from ark_amd.optimizer import ParamSet
+    ps = _params(ODD, 4)
+    tens = ckpt.param_tensors(ps)
+    nb = ckpt.image_bytes(tens)
+    one = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    ckpt.pack(tens, one, 77, 66)
+    monkeypatch.setenv("ARK_CKPT_LAUNCH_BLOCKS", per_launch)
+    split = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    ckpt.pack(tens, split, 77, 66)
+    assert torch.equal(one, split)
+    qs = ParamSet(ODD.tensors(), weight_decay=0.1)
+    ckpt.unpack(split, ckpt.param_tensors(qs))
+    for a, b in zip(tens, ckpt.param_tensors(qs)):
+        if a.element_size() == 4:
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        else:
+            np.testing.assert_array_equal(_bits(b), _quiet16(_bits(a)))
+
+
 def test_resume_is_bit_continuous(tmp_path):
     """Train, save (V4 with the AMP trailer), load into fresh buffers and a
     fresh optimizer, continue: the weights, moments and scaler state equal an
