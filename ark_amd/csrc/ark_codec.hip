@@ -38,6 +38,11 @@ struct Shape {
   static_assert(kBlocksPerSeg * kSpan == kSeg, "segment shape");
 };
 constexpr uint32_t kMaxBlocksPerSeg = Shape<ARK_CODEC_F16_TO_F32>::kBlocksPerSeg;  // 8
+static_assert(Shape<ARK_CODEC_F16_TO_F32>::kBlocksPerSeg * Shape<ARK_CODEC_F16_TO_F32>::kLanes ==
+                  Shape<ARK_CODEC_F32_TO_F16>::kBlocksPerSeg * Shape<ARK_CODEC_F32_TO_F16>::kLanes,
+              "both directions launch the same work-items per segment");
+constexpr uint64_t kMaxPlanSegs =
+    ((1ull << 32) - 1) / (kMaxBlocksPerSeg * Shape<ARK_CODEC_F16_TO_F32>::kLanes);
 
 struct CodecSeg {
   const void* src;
@@ -201,8 +206,11 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      if (segs.size() > 0x7FFFFFFFu / kMaxBlocksPerSeg)
-        return ark::fail(ARK_OPT_EINVAL, "too many elements");
+      // one launch covers every segment with 512 work-items each, and a
+      // launch's work-items stay below 2^32
+      if (segs.size() > kMaxPlanSegs)
+        return ark::fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
+                         (unsigned long long)kMaxPlanSegs, kSeg);
     }
   }
   ark_codec_plan* p = new ark_codec_plan();

@@ -585,6 +585,7 @@ __global__ __launch_bounds__(kTileCols) void run_kernel(float* __restrict__ g, u
 }
 
 constexpr uint64_t kMaxFlatBlocks = 1u << 20;
+constexpr uint64_t kMaxPlanSegs = ((1ull << 32) - 1) / (kBlocksPerSeg * kWave);  // 4,194,303
 // gather_kernel and run_kernel launch one 256-lane block per token along x,
 // and a launch's work-items along one dimension must stay below 2^32.
 constexpr uint32_t kMaxTokens = (uint32_t)((1ull << 32) / kThreads) - 1u;  // 16,777,215
@@ -805,8 +806,11 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      if (segs.size() > 0x7FFFFFFFu / kBlocksPerSeg)
-        return fail(ARK_OPT_EINVAL, "too many elements");
+      // one launch covers every segment with kBlocksPerSeg waves, and a
+      // launch's work-items stay below 2^32
+      if (segs.size() > kMaxPlanSegs)
+        return fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
+                    (unsigned long long)kMaxPlanSegs, kSeg);
     }
   }
   ark_grad_plan* p = new ark_grad_plan();

@@ -325,3 +325,38 @@ def test_entry_points_reject_host_or_short_buffers():
     assert rc == _abi.EINVAL and "dx0" in msg() and "exceeds its allocation" in msg(), msg()
     torch.cuda.synchronize()
     assert torch.count_nonzero(g).item() == 0 and torch.count_nonzero(dst).item() == 0
+
+
+def test_plans_refuse_more_segments_than_one_launch_covers():
+    """A gradient plan launches 16 one-wave blocks per 4096-element segment
+    and a codec plan 512 work-items per segment, all in one launch, whose
+    work-items must stay below 2^32: 4,194,303 and 8,388,607 segments are
+    the most they take, one more is refused with ARK_OPT_EINVAL (spans may
+    share buffers, so a small allocation reaches the limit)."""
+    import ctypes as C
+    torch = _torch()
+    from ark_amd import _abi
+    from ark_amd._lib import lib
+    L = lib()
+    dst = torch.zeros(4096, device="cuda")
+    src = torch.zeros(4096, device="cuda")
+    half = torch.zeros(4096, dtype=torch.float16, device="cuda")
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for limit, make, fields in (
+            (4194303, L.ark_grad_plan_create, (dst, src)),
+            (8388607, L.ark_codec_plan_create, (half, dst))):
+        arr = np.zeros(limit + 1, dtype=[("a", "<u8"), ("b", "<u8"), ("n", "<u8")])
+        arr["a"], arr["b"], arr["n"] = fields[0].data_ptr(), fields[1].data_ptr(), 4096
+        h = C.c_void_p()
+        if make is L.ark_grad_plan_create:
+            spans = arr.ctypes.data_as(C.POINTER(_abi.GradSpan))
+            call = lambda k: make(spans, k, stream, C.byref(h))
+            destroy = L.ark_grad_plan_destroy
+        else:
+            spans = arr.ctypes.data_as(C.POINTER(_abi.CodecSpan))
+            call = lambda k: make(spans, k, _abi.CODEC_F16_TO_F32, stream, C.byref(h))
+            destroy = L.ark_codec_plan_destroy
+        assert call(limit + 1) == _abi.EINVAL
+        assert "too many elements" in L.ark_opt_last_error().decode()
+        assert call(limit) == _abi.OK, L.ark_opt_last_error().decode()
+        destroy(h)
