@@ -360,3 +360,53 @@ def test_plans_refuse_more_segments_than_one_launch_covers():
         assert "too many elements" in L.ark_opt_last_error().decode()
         assert call(limit) == _abi.OK, L.ark_opt_last_error().decode()
         destroy(h)
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_scatters_match_the_loop(case):
+    """Seeded random token scatters against the loop of bridge.m:922-928:
+    vocabularies up to 2^17 (three sort passes past one tile), widths that
+    are and are not multiples of 4 and 256, batches on both sides of the
+    one-block sort's 4096-token tile, uniform, Zipf, single-token, sorted,
+    reversed and out-of-range token draws, and embedding rows at an element
+    offset; the allocating and the no-allocation forms, bit for bit."""
+    torch = _torch()
+    from ark_amd._lib import ArkOptError
+    rng = np.random.default_rng(7000 + case)
+    vocab = int(rng.choice([1, 2, 7, 256, 1000, 32000, 70000, 1 << 17]))
+    d = int(rng.choice([1, 3, 4, 5, 64, 255, 256, 257, 768, 1024]))
+    batch = int(rng.choice([0, 1, 2, 4095, 4096, 4097, 8192, 12289, int(rng.integers(1, 20000))]))
+    d = max(1, min(d, 8_000_000 // max(batch, 1), 16_000_000 // vocab))
+    dist = str(rng.choice(["uniform", "zipf", "same", "oob", "sorted", "reversed"]))
+    if dist == "uniform":
+        t = rng.integers(0, vocab, batch)
+    elif dist == "zipf":
+        t = np.minimum(rng.zipf(1.2, batch) - 1, vocab - 1)
+    elif dist == "same":
+        t = np.full(batch, rng.integers(0, vocab))
+    elif dist == "oob":
+        t = rng.integers(0, vocab * 2 + 5, batch)
+    else:
+        t = np.sort(rng.integers(0, vocab, batch))
+        if dist == "reversed":
+            t = t[::-1]
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    dx0 = (rng.standard_normal((batch, d)) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+    base = rng.standard_normal((vocab, d)).astype(np.float32)
+    off = int(rng.choice([0, 0, 1, 3]))
+    want = base.copy()
+    oracle.embed_scatter(want, t, dx0)
+    case_info = dict(vocab=vocab, d=d, batch=batch, dist=dist, off=off)
+    for noalloc in (False, True):
+        buf = torch.zeros(vocab * d + off, device="cuda")
+        eg = buf[off:off + vocab * d].view(vocab, d)
+        eg.copy_(torch.from_numpy(base))
+        tt = torch.from_numpy(t.view(np.int32)).cuda()
+        xx = torch.from_numpy(dx0).cuda()
+        try:
+            grad.embed_scatter(eg, tt, xx, noalloc=noalloc)
+        except ArkOptError as e:
+            assert noalloc and "static scratch" in str(e), (case_info, str(e))
+            continue
+        got = eg.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (case_info, noalloc)
