@@ -140,6 +140,39 @@ def test_ragged_unaligned_tables_and_small_norm_blocks():
             r.close()
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_random_tables_fused_equals_reading(case):
+    """Seeded random fp32-gradient tables with an embedding of random width
+    (rows whole units when it is a multiple of 256, straddling units
+    otherwise) and a random token scatter: three steps with fresh backward
+    outputs, the step after the final calls equal, bit for bit, to the step
+    that reads the gradients."""
+    torch = _torch()
+    rng = np.random.default_rng(500 + case)
+    vocab = int(rng.choice([3, 100, 1000, 5000]))
+    d = int(rng.choice([1, 64, 256, 300, 512, 768]))
+    specs = [TensorSpec("embed", (vocab, d), True, False)]
+    for i in range(int(rng.integers(0, 8))):
+        n = int(rng.choice([1, 255, 256, 257, 4095, 4096, 4097, 12345, int(rng.integers(1, 30000))]))
+        specs.append(TensorSpec(f"t{i}", (n,), bool(rng.random() < 0.8), False))
+    scale = float(2.0 ** int(rng.integers(0, 17)))
+    no_unscale = tuple(s.name for s in specs[1:] if rng.random() < 0.2)
+    outs = _outs(specs, 600 + case, 1e-3, scale)
+    runs = [_Run(specs, outs, scale, no_unscale=no_unscale) for _ in range(2)]
+    batch = int(rng.choice([0, 1, 100, 4096, 5000]))
+    for k in range(3):
+        for o in outs:
+            o.normal_(0.0, float(10.0 ** rng.uniform(-5, -1)) * scale)
+        tokens = torch.from_numpy(rng.integers(0, vocab + 3, batch).astype(np.int32)).cuda()
+        dx0 = torch.randn(batch, d, device="cuda") * scale * 1e-3
+        infos = [r.step(specs, fused, (0, vocab, d, tokens, dx0))
+                 for r, fused in zip(runs, (False, True))]
+        _info_eq(infos[0], infos[1])
+        _same(runs[0], runs[1], specs)
+    for r in runs:
+        r.close()
+
+
 def test_units_are_discarded_when_the_loss_scale_or_gradients_change():
     """After the final accumulation: ark_opt_set_state and
     ark_opt_record_overflow discard the units (the loss scale they were
