@@ -177,10 +177,11 @@ int ark_opt_destroy(ark_opt_handle *h);
  * argument: a HIP graph that captured a step replays the lr it was captured
  * with (t, the bias corrections and the AMP state still advance on the
  * device), so a schedule that changes lr needs a graph per lr value, a
- * fresh capture, or ark_opt_step_lr_dev.  The step's norm pass reads the gradients, or the units the
- * hand-off's final calls wrote (include/ark_grad.h) when they are fresh; a
- * capture keeps the choice it saw, so capture the step together with the
- * final calls that feed it, or with neither. */
+ * fresh capture, or ark_opt_step_lr_dev.  The step's norm pass reads the
+ * gradients, or the units the hand-off's final calls wrote
+ * (include/ark_grad.h) when they are fresh; a capture keeps the choice it
+ * saw, so capture the step together with the final calls that feed it, or
+ * with neither. */
 int ark_opt_step(ark_opt_handle *h, float lr, ark_opt_step_info *info);
 
 /* ark_opt_step with this step's learning rate read from the device scalar
