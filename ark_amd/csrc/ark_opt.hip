@@ -60,6 +60,7 @@ struct ark_opt_handle {
   int spb = 2;
   uint32_t norm_blocks = 0;
   uint32_t nt_from = 0;  // norm blocks from here up stream past the cache
+  uint32_t sumsq_lds = 0;  // dynamic LDS per norm block (residency cap)
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
@@ -237,6 +238,13 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   const uint64_t parts = (nseg + spb - 1) / spb;
   if (parts > ark::kMaxParts)
     return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
+  // Resident norm blocks per CU; ARK_OPT_SUMSQ_BLOCKS_PER_CU=2..8 overrides
+  // it, 0 lifts the cap (a tuning knob: results do not depend on it).
+  int blocks_per_cu = hp->grad_dtype == ARK_OPT_GRAD_F16 ? ark::kSumsqBlocksPerCuF16 : 0;
+  if (const char* env = getenv("ARK_OPT_SUMSQ_BLOCKS_PER_CU")) {
+    const int v = atoi(env);
+    if (v == 0 || (v >= 2 && v <= 8)) blocks_per_cu = v;
+  }
 
   // The reference steps distinct per-tensor fields (optimizer.rs:171,
   // memory.rs:202-255), so w, m and v can never alias.  Here a tensor listed
@@ -262,6 +270,10 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
+  int lds_per_cu = 0;
+  if (blocks_per_cu)
+    ARK_HIP(hipDeviceGetAttribute(&lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                  dev));
   ark::BufferChecker checker;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
@@ -280,6 +292,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
   h->nt_from = ark::sumsq_nt_from(spb, gsz);
+  h->sumsq_lds = ark::sumsq_lds_bytes(blocks_per_cu, lds_per_cu);
 
   // One allocation: segments | partial sums | state | scalars | info | units
   size_t off = 0;
@@ -403,7 +416,8 @@ int step_impl(ark_opt_handle* h, float lr, const float* lr_dev, ark_opt_step_inf
                                        h->d_part_sum, h->stream));
     } else {
       ARK_HIP(ark::launch_sumsq(h->hp.grad_dtype, h->spb, h->norm_blocks, h->d_segs,
-                                h->nseg, h->d_state, h->d_part_sum, h->nt_from, h->stream));
+                                h->nseg, h->d_state, h->d_part_sum, h->nt_from, h->sumsq_lds,
+                                h->stream));
     }
     if (h->d_fold)
       ARK_HIP(ark::launch_fold(h->padded_parts, h->d_part_sum, h->d_fold, h->stream));

@@ -117,6 +117,49 @@ __device__ __forceinline__ double group_sum(const float (&f)[kVec], float inv_t)
   return tree8(q);
 }
 
+// The same leaves from fp16 bits when the unscale is a power of two 2^e
+// (|e| <= kPow2MaxExp): f * 2^e is then exact in fp32, so the leaf
+// (double)gu * (double)gu is (double)(f * f) * 2^(2e), and every f64 add of
+// the tree commutes with that exact scaling (no sum of such leaves leaves
+// the normal f64 range).  f * f of an 11-bit significand fits fp32's 24
+// bits, so v_fma_mix_f32 (fp16 operands, fp32 result, + 0) forms it exactly
+// in one instruction; the caller scales the group sums once.  An inf or NaN
+// gradient squares to inf or NaN, and no finite one can make the sum
+// overflow, so the block's sum alone tells whether it saw one.  3 VALU
+// instructions per element against 7 for group_sum with the per-element
+// finite test, which keeps the pass memory bound when the clock drops.
+constexpr int kPow2MaxExp = 100;
+
+__device__ __forceinline__ float sq_f16_lo(uint32_t x) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %1, 0 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x));
+  return r;
+}
+__device__ __forceinline__ float sq_f16_hi(uint32_t x) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %1, 0 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x));
+  return r;
+}
+__device__ __forceinline__ double group_sq_f16(const u32x4& r) {
+  const uint32_t x[4] = {r.x, r.y, r.z, r.w};
+  double q[kVec];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[2 * i] = (double)sq_f16_lo(x[i]);
+    q[2 * i + 1] = (double)sq_f16_hi(x[i]);
+  }
+  return tree8(q);
+}
+
+// Whether the loss scale is 2^k with |k| <= kPow2MaxExp, i.e. its
+// reciprocal 1 / scale is exactly 2^-k.  Tested on the scale's bits, so the
+// blocks' choice of path (and their loads) need not wait for the division.
+__device__ __forceinline__ bool pow2_scale(float scale) {
+  const uint32_t b = __float_as_uint(scale);
+  const uint32_t e = b >> 23;  // sign 0 and biased exponent
+  return (b & 0x007FFFFFu) == 0u && e >= 127u - kPow2MaxExp && e <= 127u + kPow2MaxExp;
+}
+
 // Transposing butterfly over the lanes of one wave: on entry every lane holds
 // W values; at step S lanes l and l^(1<<S) add the half they keep to the
 // partner's copy of it, so the sum for each value index grows as a pairwise
@@ -151,10 +194,12 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // One batch of kRed full, 16-byte aligned segments (descriptors d) into
 // vals[0, 2*kRed): every lane issues the loads of kLoad segments before using
-// any.  NT: non-temporal loads.
-template <typename GT, int kRed, int kLoad, bool NT>
+// any.  NT: non-temporal loads.  SQ16: fp16 gradients under a power-of-two
+// unscale, leaves from group_sq_f16 (no per-element finite test).
+template <typename GT, int kRed, int kLoad, bool NT, bool SQ16>
 __device__ __forceinline__ void fast_batch(const SegDesc (&dsc)[kRed], int tid, float inv,
                                            double* vals, uint32_t& bad) {
+  static_assert(!SQ16 || sizeof(GT) == 2, "fp16 gradients only");
 #pragma unroll
   for (int b = 0; b < kRed; b += kLoad) {
     typename GradIO<GT>::Raw8 raw[2 * kLoad];
@@ -169,9 +214,14 @@ __device__ __forceinline__ void fast_batch(const SegDesc (&dsc)[kRed], int tid, 
     }
 #pragma unroll
     for (int i = 0; i < 2 * kLoad; ++i) {
-      float f[kVec];
-      GradIO<GT>::unpack8(raw[i], f, bad);
-      vals[2 * b + i] = group_sum(f, inv_k[i / 2]);
+      if constexpr (SQ16) {
+        const double s = (double)inv_k[i / 2] * (double)inv_k[i / 2];  // 2^(2e), exact
+        vals[2 * b + i] = group_sq_f16(raw[i]) * s;
+      } else {
+        float f[kVec];
+        GradIO<GT>::unpack8(raw[i], f, bad);
+        vals[2 * b + i] = group_sum(f, inv_k[i / 2]);
+      }
     }
   }
 }
@@ -223,12 +273,19 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
   for (int k = 0; k < SPB; ++k)
     fast = fast && dsc[k].n == (uint32_t)kSeg && (dsc[k].flags & kSegVec) != 0u;
 
+  bool sq16 = false;
+  if constexpr (sizeof(GT) == 2) sq16 = fast && pow2_scale(loss_scale);
+
   uint32_t bad = 0;
   double vals[V];
-  if (fast && blk >= nt_from) {
-    fast_batch<GT, SPB, kLoad, true>(dsc, tid, inv, vals, bad);
+  if (sq16 && blk >= nt_from) {
+    if constexpr (sizeof(GT) == 2) fast_batch<GT, SPB, kLoad, true, true>(dsc, tid, inv, vals, bad);
+  } else if (sq16) {
+    if constexpr (sizeof(GT) == 2) fast_batch<GT, SPB, kLoad, false, true>(dsc, tid, inv, vals, bad);
+  } else if (fast && blk >= nt_from) {
+    fast_batch<GT, SPB, kLoad, true, false>(dsc, tid, inv, vals, bad);
   } else if (fast) {
-    fast_batch<GT, SPB, kLoad, false>(dsc, tid, inv, vals, bad);
+    fast_batch<GT, SPB, kLoad, false, false>(dsc, tid, inv, vals, bad);
   } else {
     // some segment ragged, unaligned or past the end: full aligned segments
     // still take the vector loads, the rest go element by element
@@ -275,7 +332,9 @@ __global__ __launch_bounds__(kBlock) void sumsq_kernel(
     // pairwise over the V half-segment sums in lane (= index) order
 #pragma unroll
     for (int st = 0; st < log2i(V); ++st) x = x + __shfl_xor(x, 1 << st);
-    if (tid == 0) part_sum[blk] = any_bad ? __builtin_nan("") : x;
+    // sq16 blocks: a non-finite sum is exactly a non-finite gradient
+    const bool nonfinite = any_bad || (sq16 && !__builtin_isfinite(x));
+    if (tid == 0) part_sum[blk] = nonfinite ? __builtin_nan("") : x;
   }
 }
 
@@ -679,10 +738,11 @@ hipError_t launch_fold(uint32_t padded_parts, const double* in, double* out,
 
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
                         const SegDesc* segs, uint32_t nseg, const ark_opt_state* state,
-                        double* part_sum, uint32_t nt_from, hipStream_t stream) {
+                        double* part_sum, uint32_t nt_from, uint32_t lds_bytes,
+                        hipStream_t stream) {
   const dim3 grid(nblocks), block(kBlock);
-#define ARK_SUMSQ(GT, SPB)                                                        \
-  hipLaunchKernelGGL((sumsq_kernel<GT, SPB>), grid, block, 0, stream, segs, nseg, \
+#define ARK_SUMSQ(GT, SPB)                                                                \
+  hipLaunchKernelGGL((sumsq_kernel<GT, SPB>), grid, block, lds_bytes, stream, segs, nseg, \
                      state, part_sum, nt_from)
   switch (spb * 2 + (grad_dtype == ARK_OPT_GRAD_F16 ? 0 : 1)) {
     case 2: ARK_SUMSQ(uint16_t, 1); break;

@@ -125,10 +125,29 @@ static_assert(kMaxParts / kFoldGroup <= kFinTarget, "one fold leaves the finaliz
 // part_sum: one partial per block (NaN when the block saw a non-finite
 // gradient).  A batch of segments whose segments all exist, hold kSeg
 // elements and carry kSegVec takes 16-byte loads.  Blocks b >= nt_from read
-// with non-temporal loads (see sumsq_nt_from).
+// with non-temporal loads (see sumsq_nt_from).  lds_bytes of dynamic LDS per
+// block (unused by the kernel) bound how many blocks a CU holds at once (see
+// sumsq_lds_bytes).
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
                         const SegDesc* segs, uint32_t nseg, const ark_opt_state* state,
-                        double* part_sum, uint32_t nt_from, hipStream_t stream);
+                        double* part_sum, uint32_t nt_from, uint32_t lds_bytes,
+                        hipStream_t stream);
+
+// Resident norm blocks per CU for fp16 gradients.  Their fast path (squares
+// straight from the fp16 bits under a power-of-two loss scale) has so little
+// arithmetic per byte that 8 blocks per CU, the wave-slot limit, issue loads
+// faster than HBM returns them: on MI355X the pass over EKO-237M's 474 MB
+// takes 79.0-79.5 us at 8 blocks per CU, 77.2-77.5 at 7 and 78.9-79.1 at 6,
+// and over the 1.3B set's 2.56 GB 372.6 us at 7 against 379.1 at 8.  The cap
+// is set by a dynamic-LDS reservation.  0 = no cap (fp32 gradients).
+constexpr int kSumsqBlocksPerCuF16 = 7;
+// The reservation that leaves room for exactly `blocks` blocks in a CU of
+// lds_per_cu bytes: 2/(2*blocks + 1) of it, between 1/(blocks + 1) and
+// 1/blocks, so the allocation granule (2 KiB here) cannot tip the count.
+inline uint32_t sumsq_lds_bytes(int blocks, int lds_per_cu) {
+  if (blocks <= 0 || lds_per_cu <= 0) return 0;
+  return (uint32_t)((uint64_t)lds_per_cu * 2u / (2u * (uint64_t)blocks + 1u));
+}
 
 // The norm pass leaves the last kNormCachedBytes it reads (its lowest
 // blocks, where the AdamW pass starts) in the Infinity Cache and streams the

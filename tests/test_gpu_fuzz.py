@@ -18,6 +18,8 @@ and runs five steps with fresh gradients and a fresh lr each; gradient
 scales reach fp16 overflow (inf: a skipped step), and an inf, -inf or NaN is
 sometimes planted.  Every step's status and scalars and every w/m/v element
 are compared (optimizer.rs:126-228, training.rs:289-326, opti.s:192-360).
+The twenty fp16 cases run again at 1.5 times their drawn loss scale, so the
+norm pass's path for scales that are not powers of two is compared too.
 A CPU test replays every case through the oracle alone and checks that the
 sweep reaches each of those outcomes.  A last test steps 3001 tensors, most
 of them tiny."""
@@ -61,14 +63,15 @@ def _draw_grads(rng, n, grad_dtype, scale):
 CASES = 60
 
 
-def draw_case(case):
+def draw_case(case, scale_mul=1.0):
     """The case's hyperparameters, tensors (host arrays and element offsets)
-    and its per-step gradients and lrs, all from the case's seed."""
+    and its per-step gradients and lrs, all from the case's seed; the drawn
+    initial loss scale (a power of two) times scale_mul."""
     from ark_amd.optimizer import AdamConfig, AmpConfig
     rng = np.random.default_rng(1000 + case)
     grad_dtype = _abi.GRAD_F16 if case % 3 else _abi.GRAD_F32
     ntens = int(rng.integers(1, 10))
-    scale = float(2.0 ** int(rng.integers(0, 17)))
+    scale = float(2.0 ** int(rng.integers(0, 17))) * scale_mul
     cfg = AdamConfig(lr=3e-4,
                      beta1=float(np.float32(rng.choice([0.0, 0.5, 0.9, rng.uniform(0, 0.999)]))),
                      beta2=float(np.float32(rng.choice([0.0, 0.95, 0.999,
@@ -110,9 +113,22 @@ def _host_tensors(tensors, steps):
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", range(CASES))
 def test_random_tables_and_hyperparameters(case):
+    _run_case(case)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(1, CASES, 3))
+def test_random_fp16_cases_at_scales_that_are_not_powers_of_two(case):
+    """The fp16-gradient cases again with 1.5 times the drawn loss scale: the
+    norm pass then unscales each element before squaring instead of taking
+    the squares from the fp16 bits, and tests each element for inf/NaN."""
+    _run_case(case, scale_mul=1.5)
+
+
+def _run_case(case, scale_mul=1.0):
     torch = _torch()
     from ark_amd.optimizer import Optimizer
-    grad_dtype, cfg, amp, tensors, steps = draw_case(case)
+    grad_dtype, cfg, amp, tensors, steps = draw_case(case, scale_mul)
     gdt = torch.int16 if grad_dtype == _abi.GRAD_F16 else torch.float32
     as_torch = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a)
     bufs, arr = [], (_abi.Tensor * len(tensors))()

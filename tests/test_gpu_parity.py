@@ -110,19 +110,25 @@ def test_config1_layer_hundred_steps_bit_exact():
 @pytest.mark.parametrize("grad_dtype", [_abi.GRAD_F16, _abi.GRAD_F32])
 def test_norm_blocking_does_not_change_bits(grad_dtype, monkeypatch):
     """1, 2, 4 or 8 segments per norm block (with ragged and unaligned
-    tensors, so fast and element-wise blocks mix) give the same bits: the
-    sum follows the canonical tree whatever the blocking."""
+    tensors, so fast and element-wise blocks mix), and any cap on the norm
+    blocks a CU holds at once, give the same bits: the sum follows the
+    canonical tree whatever the blocking and residency."""
     torch = _torch()
     specs = config_tensors("c1") + [TensorSpec("r", (4096 * 70 + 3,), True, False),
                                     TensorSpec("s", (5,), False, True)]
     sig = [1e-3] * len(specs)
     base = None
-    for spb in ("1", "2", "4", "8"):
+    for spb, cap in (("1", None), ("2", None), ("4", None), ("8", None),
+                     ("2", "0"), ("2", "2"), ("8", "2"), ("2", "8")):
         monkeypatch.setenv("ARK_OPT_SUMSQ_SPB", spb)
+        if cap is None:
+            monkeypatch.delenv("ARK_OPT_SUMSQ_BLOCKS_PER_CU", raising=False)
+        else:
+            monkeypatch.setenv("ARK_OPT_SUMSQ_BLOCKS_PER_CU", cap)
         cfg, ps, ts, opt, ref = _make(specs, 21, sig, 4096.0, grad_dtype=grad_dtype)
         _, gi = opt.step_all(cfg.lr, info=True)
         _, ri = ref.step(cfg.lr)
-        assert not H.info_matches(gi, ri), spb
+        assert not H.info_matches(gi, ri), (spb, cap)
         base = base or gi.grad_sumsq
         assert gi.grad_sumsq == base
         opt.close()
@@ -229,13 +235,17 @@ def test_growth_cap_and_early_stop():
     opt.close()
 
 
-def test_finite_flag_every_fp16_pattern():
+@pytest.mark.parametrize("scale", [1.0, 3.0])
+def test_finite_flag_every_fp16_pattern(scale):
     """training.rs:291 on the device, exhaustively: each of the 2048 inf/NaN
     fp16 patterns, alone among zeros, makes the step skip -- placed in a
     tensor of eight full segments (one norm block of vector loads) or in a
     ragged one (mixed block, element-wise tail) at varying positions; and a
     tensor holding all 63,488 finite patterns applies, with every scalar and
-    every w/m/v bit equal to the oracle's."""
+    every w/m/v bit equal to the oracle's.  At a power-of-two loss scale
+    (full blocks take the squares from the fp16 bits and find a non-finite
+    gradient from their sum) and at one that is not (a per-element test);
+    the minimum scale keeps the skips from halving it."""
     torch = _torch()
     from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
     allp = np.arange(65536, dtype=np.uint32).astype(np.uint16)
@@ -243,7 +253,8 @@ def test_finite_flag_every_fp16_pattern():
     finite = allp[(allp & 0x7C00) != 0x7C00]
     assert nonfin.size == 2048 and finite.size == 63488
     cfg = AdamConfig(**HP)
-    amp = AmpConfig(loss_scale_init=1.0, max_consecutive_nonfinite=1 << 30)
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_min=scale,
+                    max_consecutive_nonfinite=1 << 30)
     specs = [TensorSpec("full", (8 * 4096,), True, False), TensorSpec("ragged", (4133,), True, False)]
     ps = ParamSet(specs, cfg.weight_decay)
     opt = Optimizer(cfg, ps, amp)
@@ -269,7 +280,7 @@ def test_finite_flag_every_fp16_pattern():
     ps.g(0).copy_(torch.from_numpy(g.view(np.int16)).view(torch.float16))
     ts = [oracle.HostTensor(w.copy(), g.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32),
                             cfg.weight_decay)]
-    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=1.0))
+    opt = Optimizer(cfg, ps, AmpConfig(loss_scale_init=scale, loss_scale_min=scale))
     ref = oracle.Optimizer(ts, opt.hp)
     _, gi = opt.step_all(cfg.lr, info=True)
     _, ri = ref.step(cfg.lr)
@@ -277,6 +288,54 @@ def test_finite_flag_every_fp16_pattern():
     assert not H.info_matches(gi, ri)
     c = H.compare(ps, ts)
     assert c["w"] == c["m"] == c["v"] == 0, c
+    opt.close()
+
+
+# Powers of two inside and just outside 2^-100..2^100 (the norm pass takes
+# the squares straight from the fp16 bits inside that range and unscales
+# each element first outside it) and scales that are not powers of two.
+NORM_SCALES = [1.0, 65536.0, 2.0 ** -20, 2.0 ** 100, 2.0 ** -100, 2.0 ** 101, 2.0 ** -101,
+               3.0, 1000.0, 0.75, 65535.0]
+
+
+@pytest.mark.parametrize("scale", NORM_SCALES)
+def test_norm_bits_every_fp16_pattern_every_scale_kind(scale):
+    """The step's scalars (the f64 sum of squares included) and every w/m/v
+    bit against the oracle with all 63,488 finite fp16 gradient patterns:
+    once in 16 full aligned segments (vector loads), once in a ragged tensor
+    (element-wise tail) and once in a NO_UNSCALE tensor, at each loss scale
+    (optimizer.rs:141-146, training.rs:244)."""
+    torch = _torch()
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer, ParamSet
+    allp = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = allp[(allp & 0x7C00) != 0x7C00]
+    rng = np.random.default_rng(int(np.float64(scale).view(np.uint64) % 1000))
+    full = rng.permutation(np.concatenate([finite, np.zeros(2048, np.uint16)]))
+    grads = [full, rng.permutation(finite)[:4096 * 3 + 17], rng.permutation(finite)[:4096]]
+    specs = [TensorSpec("full", (full.size,), True, False),
+             TensorSpec("ragged", (grads[1].size,), True, False),
+             TensorSpec("gain", (4096,), False, True)]
+    cfg = AdamConfig(**HP)
+    amp = AmpConfig(loss_scale_init=scale, loss_scale_min=min(1.0, scale),
+                    loss_scale_max=2.0 ** 120)
+    ps = ParamSet(specs, cfg.weight_decay, no_unscale=("gain",))
+    ts = []
+    for i, (s, g) in enumerate(zip(specs, grads)):
+        w = (rng.standard_normal(s.n) * 0.02).astype(np.float16).view(np.uint16)
+        ps.w(i).copy_(torch.from_numpy(w.view(np.int16)).view(torch.float16))
+        ps.g(i).copy_(torch.from_numpy(g.view(np.int16)).view(torch.float16))
+        ts.append(oracle.HostTensor(w.copy(), g.copy(), np.zeros(s.n, np.float32),
+                                    np.zeros(s.n, np.float32),
+                                    cfg.weight_decay if s.decay else 0.0,
+                                    _abi.TENSOR_NO_UNSCALE if s.name == "gain" else 0))
+    opt = Optimizer(cfg, ps, amp)
+    ref = oracle.Optimizer(ts, opt.hp)
+    _, gi = opt.step_all(cfg.lr, info=True)
+    _, ri = ref.step(cfg.lr)
+    assert gi.applied == 1 and gi.nonfinite == 0, scale
+    assert not H.info_matches(gi, ri), (scale, H.info_matches(gi, ri))
+    c = H.compare(ps, ts)
+    assert c["w"] == c["m"] == c["v"] == 0, (scale, c)
     opt.close()
 
 
