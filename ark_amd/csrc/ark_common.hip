@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 #include <string>
 
 namespace ark {
@@ -132,6 +133,25 @@ DeviceGuard::DeviceGuard(int dev) {
 DeviceGuard::~DeviceGuard() {
   int cur = -1;
   if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+}
+
+int lds_per_cu(int device) {
+  constexpr int kDevices = 64;
+  static std::atomic<int> cache[kDevices];  // 0: not queried yet, -1: unknown
+  if (device < 0 || device >= kDevices) return 0;
+  int v = cache[device].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int q = 0;
+    if (hipDeviceGetAttribute(&q, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device) !=
+            hipSuccess ||
+        q <= 0) {
+      (void)hipGetLastError();
+      q = -1;
+    }
+    cache[device].store(q, std::memory_order_relaxed);
+    v = q;
+  }
+  return v > 0 ? v : 0;
 }
 
 }  // namespace ark

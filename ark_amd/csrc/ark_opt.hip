@@ -61,6 +61,7 @@ struct ark_opt_handle {
   uint32_t norm_blocks = 0;
   uint32_t nt_from = 0;  // norm blocks from here up stream past the cache
   uint32_t sumsq_lds = 0;  // dynamic LDS per norm block (residency cap)
+  uint32_t adamw_lds = 0;  // dynamic LDS per AdamW block (residency cap)
   // one device allocation carved into the pieces below
   void* dev_mem = nullptr;
   SegDesc* d_segs = nullptr;
@@ -238,12 +239,19 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   const uint64_t parts = (nseg + spb - 1) / spb;
   if (parts > ark::kMaxParts)
     return fail(ARK_OPT_EINVAL, "too many elements (%llu segments)", (unsigned long long)nseg);
-  // Resident norm blocks per CU; ARK_OPT_SUMSQ_BLOCKS_PER_CU=2..8 overrides
-  // it, 0 lifts the cap (a tuning knob: results do not depend on it).
-  int blocks_per_cu = hp->grad_dtype == ARK_OPT_GRAD_F16 ? ark::kSumsqBlocksPerCuF16 : 0;
+  // Resident blocks per CU of the norm and AdamW passes;
+  // ARK_OPT_SUMSQ_BLOCKS_PER_CU=2..8 and ARK_OPT_ADAMW_BLOCKS_PER_CU=4..32
+  // override them, 0 lifts a cap (tuning knobs: results do not depend on
+  // them).
+  int sumsq_per_cu = hp->grad_dtype == ARK_OPT_GRAD_F16 ? ark::kSumsqBlocksPerCuF16 : 0;
   if (const char* env = getenv("ARK_OPT_SUMSQ_BLOCKS_PER_CU")) {
     const int v = atoi(env);
-    if (v == 0 || (v >= 2 && v <= 8)) blocks_per_cu = v;
+    if (v == 0 || (v >= 2 && v <= 8)) sumsq_per_cu = v;
+  }
+  int adamw_per_cu = ark::kAdamwBlocksPerCu;
+  if (const char* env = getenv("ARK_OPT_ADAMW_BLOCKS_PER_CU")) {
+    const int v = atoi(env);
+    if (v == 0 || (v >= 4 && v <= 32)) adamw_per_cu = v;
   }
 
   // The reference steps distinct per-tensor fields (optimizer.rs:171,
@@ -270,10 +278,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
-  int lds_per_cu = 0;
-  if (blocks_per_cu)
-    ARK_HIP(hipDeviceGetAttribute(&lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
-                                  dev));
+  const int lds_per_cu = ark::lds_per_cu(dev);
   ark::BufferChecker checker;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
@@ -292,7 +297,8 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
   h->nt_from = ark::sumsq_nt_from(spb, gsz);
-  h->sumsq_lds = ark::sumsq_lds_bytes(blocks_per_cu, lds_per_cu);
+  h->sumsq_lds = ark::resident_lds_bytes(sumsq_per_cu, lds_per_cu, ark::sumsq_static_lds(spb));
+  h->adamw_lds = ark::resident_lds_bytes(adamw_per_cu, lds_per_cu, 0);
 
   // One allocation: segments | partial sums | state | scalars | info | units
   size_t off = 0;
@@ -428,7 +434,7 @@ int step_impl(ark_opt_handle* h, float lr, const float* lr_dev, ark_opt_step_inf
   if (ev) ARK_HIP(hipEventRecord(ev[2], h->stream));
   if (h->nseg) {
     ARK_HIP(ark::launch_adamw(h->hp.grad_dtype, h->d_segs, h->nseg, h->d_scal,
-                              h->hp.beta1, h->hp.beta2, h->hp.eps, h->stream));
+                              h->hp.beta1, h->hp.beta2, h->hp.eps, h->adamw_lds, h->stream));
   }
   if (ev) {
     ARK_HIP(hipEventRecord(ev[3], h->stream));

@@ -807,15 +807,15 @@ hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
 
 hipError_t launch_adamw(uint32_t grad_dtype, const SegDesc* segs, uint32_t nseg,
                         const StepScalars* scal, float beta1, float beta2,
-                        float eps, hipStream_t stream) {
+                        float eps, uint32_t lds_bytes, hipStream_t stream) {
   if ((uint64_t)nseg > kMaxSegments) return hipErrorInvalidValue;
   const dim3 grid(nseg * kRowsPerSeg), block(64);
   if (grad_dtype == ARK_OPT_GRAD_F16)
-    hipLaunchKernelGGL((adamw_kernel<uint16_t>), grid, block, 0, stream, segs, scal,
+    hipLaunchKernelGGL((adamw_kernel<uint16_t>), grid, block, lds_bytes, stream, segs, scal,
                        beta1, beta2, eps);
   else
-    hipLaunchKernelGGL((adamw_kernel<float>), grid, block, 0, stream, segs, scal, beta1,
-                       beta2, eps);
+    hipLaunchKernelGGL((adamw_kernel<float>), grid, block, lds_bytes, stream, segs, scal,
+                       beta1, beta2, eps);
   return hipGetLastError();
 }
 
