@@ -50,7 +50,7 @@ def _declare(L):
         "ark_synth_normal_f32": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_fill_u16": ([P, u64, C.c_uint16, P], C.c_int),
         "ark_synth_copy": ([P, P, u64, P], C.c_int),
-        "ark_synth_stream_mix": ([P, P, P, P, u64, u32, P], C.c_int),
+        "ark_synth_stream_mix": ([P, P, P, P, u64, u32, u32, P], C.c_int),
         "ark_hip_dequant_f16_to_f32": ([P, P, u64, P], C.c_int),
         "ark_hip_quant_f32_to_f16": ([P, P, u64, P], C.c_int),
         "ark_codec_plan_create": ([C.POINTER(_abi.CodecSpan), i32, u32, P, C.POINTER(H)],

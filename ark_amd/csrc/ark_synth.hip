@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ark_common.hpp"
 #include "ark_synth.h"
 
 namespace {
@@ -160,15 +161,18 @@ int ark_synth_copy(void* dst, const void* src, uint64_t nbytes, void* stream) {
 }
 
 int ark_synth_stream_mix(uint16_t* w, const uint16_t* g, float* m, float* v, uint64_t n,
-                         uint32_t spacing, void* stream) {
+                         uint32_t spacing, uint32_t blocks_per_cu, void* stream) {
   if (n == 0) return 0;
-  if (!w || !g || !m || !v || (n % 256u) ||
+  if (!w || !g || !m || !v || (n % 256u) || blocks_per_cu > 32u ||
       (((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u))
     return -1;
   const uint64_t rows = n / 256u;
   if (rows > 0x7FFFFFFFull / 64u) return -1;
-  hipLaunchKernelGGL(stream_mix_kernel, dim3((uint32_t)rows), dim3(64), 0, (hipStream_t)stream, w,
-                     g, m, v, spacing, 0.0f, 1.0f, 0.0f);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  const uint32_t lds = ark::resident_lds_bytes((int)blocks_per_cu, ark::lds_per_cu(dev), 0);
+  hipLaunchKernelGGL(stream_mix_kernel, dim3((uint32_t)rows), dim3(64), lds, (hipStream_t)stream,
+                     w, g, m, v, spacing, 0.0f, 1.0f, 0.0f);
   return status(hipGetLastError());
 }
 

@@ -278,5 +278,5 @@ extern "C" {
     pub fn ark_synth_copy(dst: *mut c_void, src: *const c_void, nbytes: u64,
                           stream: *mut c_void) -> c_int;
     pub fn ark_synth_stream_mix(w: *mut u16, g: *const u16, m: *mut f32, v: *mut f32, n: u64,
-                                spacing: u32, stream: *mut c_void) -> c_int;
+                                spacing: u32, blocks_per_cu: u32, stream: *mut c_void) -> c_int;
 }

@@ -49,15 +49,16 @@ def copy(dst, src):
     check(lib().ark_synth_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream(src)))
 
 
-def stream_mix(w, g, m, v, spacing):
+def stream_mix(w, g, m, v, spacing, blocks_per_cu=0):
     """The AdamW pass's accesses without its arithmetic (ark_synth_stream_mix):
     w, g 16-bit and m, v fp32 tensors of n elements (n a multiple of 256);
-    w, m and v are written back unchanged."""
+    w, m and v are written back unchanged.  blocks_per_cu: resident blocks
+    per CU (0: every wave slot)."""
     n = w.numel()
     assert all(t.is_cuda and t.is_contiguous() and t.numel() == n for t in (w, g, m, v))
     assert w.element_size() == g.element_size() == 2 and m.element_size() == v.element_size() == 4
     check(lib().ark_synth_stream_mix(w.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), n,
-                                     spacing, _stream(w)))
+                                     spacing, blocks_per_cu, _stream(w)))
 
 
 def fill_u16(t, bits):

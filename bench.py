@@ -282,11 +282,12 @@ def run_ceiling(a):
     memory as the pass: the stream-mix probe (ark_synth_stream_mix: AdamW's
     one-wave-per-row shape, seven streams and cache hints, 22 B/param, its
     arithmetic replaced by a chain of `spacing` dependent fma) run over the
-    workload's own parameter arenas.  First a spacing sweep (median of
-    --steps launches each, HIP events); then --steps rounds that each time
-    one probe launch at the best spacing and one optimizer step with the
-    handle's per-kernel events, so the probe and the AdamW pass are compared
-    interleaved on the same box and the same pages."""
+    workload's own parameter arenas.  First a sweep of spacing and of the
+    resident blocks per CU (every wave slot, 20, 16 -- the AdamW pass's --
+    and 14; median of --steps launches each, HIP events); then --steps
+    rounds that each time one probe launch at the best point and one
+    optimizer step with the handle's per-kernel events, so the probe and the
+    AdamW pass are compared interleaved on the same box and the same pages."""
     import torch
     from ark_amd import synth
     from ark_amd.eko import config_tensors
@@ -303,26 +304,29 @@ def run_ceiling(a):
               ps.m_arena[:n], ps.v_arena[:n])
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def probe(spacing):
+    def probe(spacing, per_cu):
         e0.record()
-        synth.stream_mix(*arenas, spacing)
+        synth.stream_mix(*arenas, spacing, per_cu)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)
 
     sweep = []
-    for spacing in (0, 16, 32, 64, 128, 256):
-        probe(spacing)
-        ms = sorted(probe(spacing) for _ in range(a.steps))[a.steps // 2]
-        sweep.append(dict(spacing=spacing, ms=round(ms, 4),
-                          gbs=round(22 * n / (ms * 1e-3) / 1e9, 1)))
-        log(f"[bench] stream mix spacing {spacing:4d}: {ms:.4f} ms = {sweep[-1]['gbs']} GB/s")
-    best = min(sweep, key=lambda r: r["ms"])["spacing"]
+    for per_cu in (0, 20, 16, 14):
+        for spacing in (0, 16, 32, 64, 128, 256):
+            probe(spacing, per_cu)
+            ms = sorted(probe(spacing, per_cu) for _ in range(a.steps))[a.steps // 2]
+            sweep.append(dict(spacing=spacing, blocks_per_cu=per_cu, ms=round(ms, 4),
+                              gbs=round(22 * n / (ms * 1e-3) / 1e9, 1)))
+            log(f"[bench] stream mix {per_cu:2d} blocks per CU, spacing {spacing:4d}: "
+                f"{ms:.4f} ms = {sweep[-1]['gbs']} GB/s")
+    best_pt = min(sweep, key=lambda r: r["ms"])
+    best, best_cu = best_pt["spacing"], best_pt["blocks_per_cu"]
     for _ in range(3):
         opt.step_all(cfg.lr)
     probe_ms, adam_ms = [], []
     for _ in range(a.steps):
-        probe_ms.append(probe(best))
+        probe_ms.append(probe(best, best_cu))
         opt.set_timing(True)
         opt.step_all(cfg.lr)
         torch.cuda.synchronize()
@@ -341,7 +345,7 @@ def run_ceiling(a):
         "scaling": "weak", "vs_baseline": None, "dtype": "u16/f32 copy", "data": "synthetic",
         "config": {"workload": f"{name}: the optimizer's parameter arenas ({n} elements; "
                                f"{n_params} params)",
-                   "sweep": sweep, "best_spacing": best,
+                   "sweep": sweep, "best_spacing": best, "best_blocks_per_cu": best_cu,
                    "interleaved": {"probe_ms": round(pm, 4), "adamw_ms": round(am, 4),
                                    "adamw_gbs": round(22 * n_params / (am * 1e-3) / 1e9, 1),
                                    "adamw_over_probe_per_element":

@@ -56,10 +56,12 @@ int ark_synth_copy(void *dst, const void *src, uint64_t nbytes, void *stream);
  * and v back unchanged, with the same instructions and cache hints, and a
  * chain of `spacing` dependent fp32 fma between the loads and the stores in
  * place of the element math.  22 bytes per element, the pass's stream mix:
- * the measured ceiling for that access pattern.  n a multiple of 256, every
- * pointer 16-byte aligned; returns -1 otherwise. */
+ * the measured ceiling for that access pattern.  blocks_per_cu (at most 32)
+ * caps the one-wave blocks resident per CU with a dynamic-LDS reservation, as
+ * the optimizer holds its AdamW pass; 0 leaves every wave slot open.  n a
+ * multiple of 256, every pointer 16-byte aligned; returns -1 otherwise. */
 int ark_synth_stream_mix(uint16_t *w, const uint16_t *g, float *m, float *v, uint64_t n,
-                         uint32_t spacing, void *stream);
+                         uint32_t spacing, uint32_t blocks_per_cu, void *stream);
 
 #ifdef __cplusplus
 }

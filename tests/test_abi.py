@@ -178,11 +178,12 @@ def test_synth_argument_checks():
     assert L.ark_synth_normal_f16(None, 0, 1, 2, 3, 1.0, None) == 0
     assert L.ark_synth_normal_f16(None, 5, 1, 2, 3, 1.0, None) == -1
     sm = L.ark_synth_stream_mix
-    assert sm(None, None, None, None, 0, 0, None) == 0
-    assert sm(0x1000, 0x2000, 0x3000, 0x4000, 300, 0, None) == -1  # not a multiple of 256
-    assert sm(0x1000, 0x2008, 0x3000, 0x4000, 256, 0, None) == -1  # not 16-byte aligned
-    assert sm(None, 0x2000, 0x3000, 0x4000, 256, 0, None) == -1
-    assert sm(0x1000, 0x2000, 0x3000, 0x4000, 2 ** 50, 0, None) == -1  # grid too large
+    assert sm(None, None, None, None, 0, 0, 0, None) == 0
+    assert sm(0x1000, 0x2000, 0x3000, 0x4000, 300, 0, 0, None) == -1  # not a multiple of 256
+    assert sm(0x1000, 0x2008, 0x3000, 0x4000, 256, 0, 0, None) == -1  # not 16-byte aligned
+    assert sm(None, 0x2000, 0x3000, 0x4000, 256, 0, 0, None) == -1
+    assert sm(0x1000, 0x2000, 0x3000, 0x4000, 2 ** 50, 0, 0, None) == -1  # grid too large
+    assert sm(0x1000, 0x2000, 0x3000, 0x4000, 256, 0, 33, None) == -1  # more than 32 per CU
 
 
 def test_handle_calls_reject_null():

@@ -134,6 +134,20 @@ def test_norm_blocking_does_not_change_bits(grad_dtype, monkeypatch):
         opt.close()
 
 
+@pytest.mark.parametrize("cap", ["0", "4", "16", "32"])
+def test_adamw_residency_does_not_change_bits(cap, monkeypatch):
+    """Any cap on the one-wave AdamW blocks a CU holds at once (none, the
+    fewest allowed, the default, every wave slot) gives every w/m/v bit of
+    the oracle's, on ragged and unaligned tensors too."""
+    monkeypatch.setenv("ARK_OPT_ADAMW_BLOCKS_PER_CU", cap)
+    specs = config_tensors("c1") + [TensorSpec("r", (4096 * 5 + 3,), True, False),
+                                    TensorSpec("s", (5,), False, True)]
+    sig = [1e-3] * len(specs)
+    cfg, ps, ts, opt, ref = _make(specs, 31, sig, 2048.0)
+    _run_steps(ps, ts, opt, ref, 31, sig, 2048.0, 2, cfg.lr)
+    opt.close()
+
+
 def test_ragged_and_tiny_tensors():
     specs = [TensorSpec("a", (1,), True, False), TensorSpec("b", (7,), False, True),
              TensorSpec("c", (4095,), True, False), TensorSpec("d", (4097,), True, False),
