@@ -154,4 +154,43 @@ int lds_per_cu(int device) {
   return v > 0 ? v : 0;
 }
 
+uint32_t resident_lds_bytes(const void* kernel, int threads, int blocks) {
+  if (blocks <= 0) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const uint32_t lds = (uint32_t)lds_per_cu(dev);
+  if (lds == 0) return 0;
+  // resident blocks with `dyn` bytes reserved (0 when it cannot launch)
+  auto occ = [&](uint32_t dyn, int* n) {
+    *n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(n, kernel, threads, dyn) != hipSuccess) {
+      (void)hipGetLastError();
+      *n = 0;
+      return false;
+    }
+    return true;
+  };
+  int n0 = 0;
+  if (!occ(0, &n0) || n0 <= blocks) return 0;
+  // smallest reservation in (0, lds] that leaves at most b blocks
+  auto first_at_most = [&](int b) {
+    uint32_t lo = 0, hi = lds;  // occupancy(lo) > b >= occupancy(hi)
+    while (hi - lo > 1) {
+      const uint32_t mid = lo + (hi - lo) / 2;
+      int n = 0;
+      occ(mid, &n);
+      if (n <= b)
+        hi = mid;
+      else
+        lo = mid;
+    }
+    return hi;
+  };
+  const uint32_t a = first_at_most(blocks), z = first_at_most(blocks - 1);
+  return a + (z - a) / 2;
+}
+
 }  // namespace ark

@@ -75,21 +75,19 @@ int check_disjoint(std::vector<Span> written, std::vector<Span> readonly);
 // Residency caps for streaming kernels.  A streaming kernel that fills every
 // wave slot of a CU issues more loads than HBM serves best on MI355X; fewer
 // resident blocks per CU run faster (the cap of each kernel is measured where
-// it is set).  The cap is a dynamic-LDS reservation the kernel never touches:
-// a CU holds floor(lds_per_cu / allocation) blocks, each allocation being the
-// block's static plus dynamic LDS rounded up to kLdsGranule.
-constexpr uint32_t kLdsGranule = 1024;  // gfx950: 10241-11264 B reserve alike
+// it is set).  The cap is a dynamic-LDS reservation the kernel never touches.
+//
 // The device's LDS per CU (163,840 B on MI355X), queried once per device; 0
 // when the runtime cannot tell.
 int lds_per_cu(int device);
-// Dynamic LDS that makes each block's allocation exactly
-// floor(lds_per_cu / blocks) rounded down to the granule, so a CU holds
-// `blocks` of them; 0 (no cap) when blocks <= 0 or the size is unknown.
-inline uint32_t resident_lds_bytes(int blocks, int lds_per_cu, uint32_t static_bytes) {
-  if (blocks <= 0 || lds_per_cu <= 0) return 0;
-  const uint32_t total = (uint32_t)lds_per_cu / (uint32_t)blocks / kLdsGranule * kLdsGranule;
-  return total > static_bytes ? total - static_bytes : 0;
-}
+// The reservation that leaves `blocks` resident blocks per CU of `kernel`
+// launched with `threads` threads on the current device, by the runtime's
+// occupancy calculator (which counts the kernel's own LDS, including what
+// library calls such as __syncthreads_or add, and the allocation granule):
+// the middle of the range of reservations that give that count.  0 when
+// blocks <= 0, the kernel holds no more than that anyway, or the runtime
+// cannot tell.
+uint32_t resident_lds_bytes(const void* kernel, int threads, int blocks);
 
 // Scratch device memory from the stream-ordered pool, freed in stream order
 // when the owner goes out of scope (after the work queued on it).

@@ -278,7 +278,6 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
-  const int lds_per_cu = ark::lds_per_cu(dev);
   ark::BufferChecker checker;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
@@ -297,8 +296,8 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   h->spb = spb;
   h->norm_blocks = (uint32_t)parts;
   h->nt_from = ark::sumsq_nt_from(spb, gsz);
-  h->sumsq_lds = ark::resident_lds_bytes(sumsq_per_cu, lds_per_cu, ark::sumsq_static_lds(spb));
-  h->adamw_lds = ark::resident_lds_bytes(adamw_per_cu, lds_per_cu, 0);
+  h->sumsq_lds = ark::sumsq_lds_for(hp->grad_dtype, spb, sumsq_per_cu);
+  h->adamw_lds = ark::adamw_lds_for(hp->grad_dtype, adamw_per_cu);
 
   // One allocation: segments | partial sums | state | scalars | info | units
   size_t off = 0;

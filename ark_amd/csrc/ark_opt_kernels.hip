@@ -16,6 +16,7 @@
 // Infinity Cache for the AdamW pass that starts on them right after (~5 %
 // faster AdamW on EKO-237M, within one step, so real training sees it too),
 // and streams the rest with non-temporal loads (13 % faster reads).
+#include "ark_common.hpp"
 #include "ark_device.hpp"
 #include "ark_opt_internal.hpp"
 #include "ark_opt_kernels.hpp"
@@ -775,6 +776,25 @@ hipError_t launch_units_reduce(int spb, uint32_t nblocks, const double* units,
   }
 #undef ARK_UNITS
   return hipGetLastError();
+}
+
+uint32_t sumsq_lds_for(uint32_t grad_dtype, int spb, int blocks) {
+  const bool f16 = grad_dtype == ARK_OPT_GRAD_F16;
+  const void* k = nullptr;
+  switch (spb) {
+    case 1: k = f16 ? (const void*)sumsq_kernel<uint16_t, 1> : (const void*)sumsq_kernel<float, 1>; break;
+    case 2: k = f16 ? (const void*)sumsq_kernel<uint16_t, 2> : (const void*)sumsq_kernel<float, 2>; break;
+    case 4: k = f16 ? (const void*)sumsq_kernel<uint16_t, 4> : (const void*)sumsq_kernel<float, 4>; break;
+    case 8: k = f16 ? (const void*)sumsq_kernel<uint16_t, 8> : (const void*)sumsq_kernel<float, 8>; break;
+    default: return 0;
+  }
+  return resident_lds_bytes(k, kBlock, blocks);
+}
+
+uint32_t adamw_lds_for(uint32_t grad_dtype, int blocks) {
+  const void* k = grad_dtype == ARK_OPT_GRAD_F16 ? (const void*)adamw_kernel<uint16_t>
+                                                 : (const void*)adamw_kernel<float>;
+  return resident_lds_bytes(k, 64, blocks);
 }
 
 uint32_t finalize_leaves(uint32_t nparts) {

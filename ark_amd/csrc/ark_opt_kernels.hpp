@@ -127,7 +127,7 @@ static_assert(kMaxParts / kFoldGroup <= kFinTarget, "one fold leaves the finaliz
 // elements and carry kSegVec takes 16-byte loads.  Blocks b >= nt_from read
 // with non-temporal loads (see sumsq_nt_from).  lds_bytes of dynamic LDS per
 // block (unused by the kernel) bound how many blocks a CU holds at once
-// (resident_lds_bytes).
+// (sumsq_lds_for).
 hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
                         const SegDesc* segs, uint32_t nseg, const ark_opt_state* state,
                         double* part_sum, uint32_t nt_from, uint32_t lds_bytes,
@@ -139,19 +139,20 @@ hipError_t launch_sumsq(uint32_t grad_dtype, int spb, uint32_t nblocks,
 // faster than HBM returns them: on MI355X the pass over EKO-237M's 474 MB
 // takes 79.0-79.5 us at 8 blocks per CU, 77.2-77.5 at 7 and 78.9-79.1 at 6,
 // and over the 1.3B set's 2.56 GB 372.6 us at 7 against 379.1 at 8.  0 = no
-// cap (fp32 gradients).  Set through resident_lds_bytes.
+// cap (fp32 gradients).
 constexpr int kSumsqBlocksPerCuF16 = 7;
-// The norm kernel's static LDS (one double per wave and half-segment value).
-constexpr uint32_t sumsq_static_lds(int spb) {
-  return (uint32_t)(sizeof(double) * (kBlock / 64) * 2 * spb);
-}
+// The dynamic LDS that holds the norm kernel for (grad_dtype, spb) at
+// `blocks` per CU (resident_lds_bytes; 0 = no cap).
+uint32_t sumsq_lds_for(uint32_t grad_dtype, int spb, int blocks);
 // Resident one-wave AdamW blocks per CU.  32 (every wave slot) over-issue
 // the pass's seven streams: on MI355X the EKO-237M pass takes 783.5 us
-// unbounded, 776.6 at 26 per CU, 762.5 at 20, 760.5 at 16, 768 at 14 and
-// 782 at 13; the 1.3B set's 4480 us unbounded, 4351 at 20, 4310-4323 at 16
-// and 4284 at 14.  Set through resident_lds_bytes (the kernel has no static
-// LDS).
+// unbounded, 776.6 at 26 per CU, 762.5 at 20, 760.4-760.6 at 17 and 16,
+// 768 at 15 and 14 and 782 at 13; the 1.3B set's 4465-4480 us unbounded,
+// 4351 at 20, 4310-4323 at 17 and 16, 4283-4285 at 15 and 14.
 constexpr int kAdamwBlocksPerCu = 16;
+// The dynamic LDS that holds the AdamW kernel for grad_dtype at `blocks` per
+// CU (resident_lds_bytes; 0 = no cap).
+uint32_t adamw_lds_for(uint32_t grad_dtype, int blocks);
 
 // The norm pass leaves the last kNormCachedBytes it reads (its lowest
 // blocks, where the AdamW pass starts) in the Infinity Cache and streams the
@@ -175,7 +176,7 @@ hipError_t launch_finalize(uint32_t leaves, const double* part_sum,
                            ark_opt_state* state, StepScalars* scal,
                            ark_opt_step_info* info, hipStream_t stream);
 
-// lds_bytes: dynamic LDS per block, the residency cap (resident_lds_bytes).
+// lds_bytes: dynamic LDS per block, the residency cap (adamw_lds_for).
 hipError_t launch_adamw(uint32_t grad_dtype, const SegDesc* segs,
                         uint32_t nseg, const StepScalars* scal, float beta1,
                         float beta2, float eps, uint32_t lds_bytes, hipStream_t stream);

@@ -168,9 +168,8 @@ int ark_synth_stream_mix(uint16_t* w, const uint16_t* g, float* m, float* v, uin
     return -1;
   const uint64_t rows = n / 256u;
   if (rows > 0x7FFFFFFFull / 64u) return -1;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return -1;
-  const uint32_t lds = ark::resident_lds_bytes((int)blocks_per_cu, ark::lds_per_cu(dev), 0);
+  const uint32_t lds =
+      ark::resident_lds_bytes((const void*)stream_mix_kernel, 64, (int)blocks_per_cu);
   hipLaunchKernelGGL(stream_mix_kernel, dim3((uint32_t)rows), dim3(64), lds, (hipStream_t)stream,
                      w, g, m, v, spacing, 0.0f, 1.0f, 0.0f);
   return status(hipGetLastError());
