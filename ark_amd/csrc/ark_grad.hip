@@ -48,10 +48,12 @@ constexpr int kPerLane = 4;
 constexpr uint32_t kSeg = 4096;
 constexpr int kWave = 64;
 constexpr uint32_t kBlocksPerSeg = kSeg / (kWave * kPerLane);  // 16
-// Resident one-wave plan blocks per CU (grad_batch, grad_batch_units), held
-// by a dynamic-LDS reservation the kernels never touch.  On MI355X the
-// accumulation over EKO-237M's 272 gradients takes 0.4270 ms with every wave
-// slot (32 per CU), 0.4226-0.4237 ms at 22-28 per CU and 0.434 ms at 20.
+// Resident one-wave grad_batch blocks per CU, held by a dynamic-LDS
+// reservation the kernel never touches.  On MI355X the accumulation over
+// EKO-237M's 272 gradients takes 0.4270 ms with every wave slot (32 per CU),
+// 0.4226-0.4237 ms at 22-28 per CU and 0.434 ms at 20.  grad_batch_units keeps
+// every slot: its per-wave tree of squares shows at fewer waves (470.7
+// against 443.0 us at 24 per CU, same box).
 constexpr int kPlanBlocksPerCu = 24;
 constexpr int kTileCols = 256;  // run_kernel: columns per block
 constexpr int kLongRun = 8;     // runs of at least this many rows: one column per lane
@@ -755,8 +757,7 @@ struct ark_grad_plan {
   hipStream_t stream = nullptr;
   uint32_t nseg = 0;
   GradSeg* d_segs = nullptr;
-  uint32_t lds = 0;        // dynamic LDS per grad_batch block (residency cap)
-  uint32_t lds_units = 0;  // the same for grad_batch_units
+  uint32_t lds = 0;  // dynamic LDS per grad_batch block (residency cap)
   std::vector<const float*> span_dst;  // the spans as given, for matching an
   std::vector<uint64_t> span_n;        // optimizer table
   std::vector<uint64_t> span_bytes;    // 4 * span_n
@@ -839,7 +840,6 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
       if (v == 0 || (v >= 8 && v <= 32)) per_cu = v;
     }
     p->lds = ark::resident_lds_bytes((const void*)grad_batch, kWave, per_cu);
-    p->lds_units = ark::resident_lds_bytes((const void*)grad_batch_units, kWave, per_cu);
   }
   if (e == hipSuccess && !segs.empty()) {
     e = hipMalloc(&p->d_segs, segs.size() * sizeof(GradSeg));
@@ -882,8 +882,8 @@ int ark_grad_plan_run_final(ark_grad_plan* p, ark_opt_handle* opt) {
   if (p->nseg) {
     ark::DeviceGuard g(p->device);
     if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
-    hipLaunchKernelGGL(grad_batch_units, dim3(p->nseg * kBlocksPerSeg), dim3(kWave),
-                       p->lds_units, p->stream, p->d_segs, U.segs, U.state, U.units);
+    hipLaunchKernelGGL(grad_batch_units, dim3(p->nseg * kBlocksPerSeg), dim3(kWave), 0,
+                       p->stream, p->d_segs, U.segs, U.state, U.units);
     ARK_HIP(hipGetLastError());
   }
   ark::opt_units_set_fresh(opt, true);
