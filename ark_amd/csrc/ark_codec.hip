@@ -186,18 +186,39 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
   const uint64_t ss = direction == ARK_CODEC_F16_TO_F32 ? 2u : 4u;
   const uint64_t ds = direction == ARK_CODEC_F16_TO_F32 ? 4u : 2u;
   std::vector<CodecSeg> segs;
-  ark::BufferChecker checker;
   int rc;
+  // One launch converts every span at once, so a dst shared with another
+  // span's dst or src would race: every dst must be disjoint from every other
+  // span (srcs may overlap each other).  Checked before any device query.
+  {
+    std::vector<ark::Span> written, readonly;
+    uint64_t nseg = 0;
+    for (int32_t i = 0; i < n_spans; ++i) {
+      const ark_codec_span& s = spans[i];
+      if (s.n == 0) continue;
+      if (((uintptr_t)s.src % ss) || ((uintptr_t)s.dst % ds))
+        return ark::fail(ARK_OPT_EINVAL, "span %d: src or dst not aligned to its element", i);
+      if (s.n > (1ull << 48)) return ark::fail(ARK_OPT_EINVAL, "span %d: n too large", i);
+      // one launch covers every segment with 512 work-items each, and a
+      // launch's work-items stay below 2^32
+      nseg += (s.n + kSeg - 1) / kSeg;
+      if (nseg > kMaxPlanSegs)
+        return ark::fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
+                         (unsigned long long)kMaxPlanSegs, kSeg);
+      if (overlaps(s.src, s.n * ss, s.dst, s.n * ds))
+        return ark::fail(ARK_OPT_EINVAL, "span %d: src and dst overlap", i);
+      written.push_back({(uintptr_t)s.dst, (uintptr_t)s.dst + s.n * ds, "dst", i});
+      readonly.push_back({(uintptr_t)s.src, (uintptr_t)s.src + s.n * ss, "src", i});
+    }
+    if ((rc = ark::check_disjoint(std::move(written), std::move(readonly), "span", "the plan")))
+      return rc;
+  }
+  ark::BufferChecker checker;
   for (int32_t i = 0; i < n_spans; ++i) {
     const ark_codec_span& s = spans[i];
     if (s.n == 0) continue;
-    if (((uintptr_t)s.src % ss) || ((uintptr_t)s.dst % ds))
-      return ark::fail(ARK_OPT_EINVAL, "span %d: src or dst not aligned to its element", i);
-    if (s.n > (1ull << 48)) return ark::fail(ARK_OPT_EINVAL, "span %d: n too large", i);
     if ((rc = checker.check(s.src, s.n * ss, "src", i))) return rc;
     if ((rc = checker.check(s.dst, s.n * ds, "dst", i))) return rc;
-    if (overlaps(s.src, s.n * ss, s.dst, s.n * ds))
-      return ark::fail(ARK_OPT_EINVAL, "span %d: src and dst overlap", i);
     const uint32_t vec = ((((uintptr_t)s.src | (uintptr_t)s.dst) & 15u) == 0) ? 1u : 0u;
     for (uint64_t off = 0; off < s.n; off += kSeg) {
       CodecSeg d;
@@ -206,11 +227,6 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      // one launch covers every segment with 512 work-items each, and a
-      // launch's work-items stay below 2^32
-      if (segs.size() > kMaxPlanSegs)
-        return ark::fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
-                         (unsigned long long)kMaxPlanSegs, kSeg);
     }
   }
   ark_codec_plan* p = new ark_codec_plan();

@@ -99,7 +99,8 @@ int BufferChecker::check(const void* p, uint64_t bytes, const char* what, int id
   return rc;
 }
 
-int check_disjoint(std::vector<Span> written, std::vector<Span> readonly) {
+int check_disjoint(std::vector<Span> written, std::vector<Span> readonly, const char* unit,
+                   const char* writer) {
   auto empty = [](const Span& x) { return x.hi <= x.lo; };
   written.erase(std::remove_if(written.begin(), written.end(), empty), written.end());
   readonly.erase(std::remove_if(readonly.begin(), readonly.end(), empty), readonly.end());
@@ -110,8 +111,8 @@ int check_disjoint(std::vector<Span> written, std::vector<Span> readonly) {
   for (size_t i = 1; i < written.size(); ++i) {
     const Span &a = written[i - 1], &b = written[i];
     if (b.lo < a.hi)
-      return fail(ARK_OPT_EINVAL, "tensor %d %s overlaps tensor %d %s (both written)", a.idx,
-                  a.what, b.idx, b.what);
+      return fail(ARK_OPT_EINVAL, "%s %d %s overlaps %s %d %s (both written)", unit, a.idx,
+                  a.what, unit, b.idx, b.what);
   }
   // disjoint and sorted: the ends are sorted too, so the first written span
   // ending past r.lo is the only candidate for overlapping r
@@ -119,8 +120,8 @@ int check_disjoint(std::vector<Span> written, std::vector<Span> readonly) {
     auto it = std::upper_bound(written.begin(), written.end(), r.lo,
                                [](uintptr_t x, const Span& s) { return x < s.hi; });
     if (it != written.end() && it->lo < r.hi)
-      return fail(ARK_OPT_EINVAL, "tensor %d %s overlaps tensor %d %s (written by the step)",
-                  r.idx, r.what, it->idx, it->what);
+      return fail(ARK_OPT_EINVAL, "%s %d %s overlaps %s %d %s (written by %s)", unit, r.idx,
+                  r.what, unit, it->idx, it->what, writer);
   }
   return ARK_OPT_OK;
 }

@@ -69,8 +69,10 @@ struct Span {
 // Fails with ARK_OPT_EINVAL, naming both buffers, when two written spans
 // share a byte or a read-only span shares a byte with a written one (read-
 // only spans may overlap each other).  Empty spans are ignored.  Host-only:
-// compares addresses, queries nothing.
-int check_disjoint(std::vector<Span> written, std::vector<Span> readonly);
+// compares addresses, queries nothing.  unit and writer word the message
+// ("tensor 3 w overlaps tensor 5 v", "... (written by the step)").
+int check_disjoint(std::vector<Span> written, std::vector<Span> readonly,
+                   const char* unit = "tensor", const char* writer = "the step");
 
 // Residency caps for streaming kernels.  A streaming kernel that fills every
 // wave slot of a CU issues more loads than HBM serves best on MI355X; fewer

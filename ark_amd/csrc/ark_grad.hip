@@ -795,18 +795,39 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
   if (n_spans < 0 || (n_spans > 0 && !spans))
     return fail(ARK_OPT_EINVAL, "span table is NULL or n_spans < 0");
   std::vector<GradSeg> segs;
-  ark::BufferChecker checker;
   int rc;
+  // One launch runs every span at once, so a dst shared with another span's
+  // dst or src would race: every dst must be disjoint from every other span
+  // (srcs may overlap each other).  Checked before any device query.
+  {
+    std::vector<ark::Span> written, readonly;
+    uint64_t nseg = 0;
+    for (int32_t i = 0; i < n_spans; ++i) {
+      const ark_grad_span& s = spans[i];
+      if (s.n == 0) continue;
+      if (((uintptr_t)s.dst & 3u) || ((uintptr_t)s.src & 3u))
+        return fail(ARK_OPT_EINVAL, "span %d: dst or src not 4-byte aligned", i);
+      if (s.n > (1ull << 48)) return fail(ARK_OPT_EINVAL, "span %d: n too large", i);
+      // one launch covers every segment with kBlocksPerSeg waves, and a
+      // launch's work-items stay below 2^32
+      nseg += (s.n + kSeg - 1) / kSeg;
+      if (nseg > kMaxPlanSegs)
+        return fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
+                    (unsigned long long)kMaxPlanSegs, kSeg);
+      if (overlaps(s.dst, s.n * 4, s.src, s.n * 4))
+        return fail(ARK_OPT_EINVAL, "span %d: dst and src overlap", i);
+      written.push_back({(uintptr_t)s.dst, (uintptr_t)s.dst + s.n * 4, "dst", i});
+      readonly.push_back({(uintptr_t)s.src, (uintptr_t)s.src + s.n * 4, "src", i});
+    }
+    if ((rc = ark::check_disjoint(std::move(written), std::move(readonly), "span", "the plan")))
+      return rc;
+  }
+  ark::BufferChecker checker;
   for (int32_t i = 0; i < n_spans; ++i) {
     const ark_grad_span& s = spans[i];
     if (s.n == 0) continue;
-    if (((uintptr_t)s.dst & 3u) || ((uintptr_t)s.src & 3u))
-      return fail(ARK_OPT_EINVAL, "span %d: dst or src not 4-byte aligned", i);
-    if (s.n > (1ull << 48)) return fail(ARK_OPT_EINVAL, "span %d: n too large", i);
     if ((rc = checker.check(s.dst, s.n * 4, "dst", i))) return rc;
     if ((rc = checker.check(s.src, s.n * 4, "src", i))) return rc;
-    if (overlaps(s.dst, s.n * 4, s.src, s.n * 4))
-      return fail(ARK_OPT_EINVAL, "span %d: dst and src overlap", i);
     const uint32_t vec = ((((uintptr_t)s.dst | (uintptr_t)s.src) & 15u) == 0) ? 1u : 0u;
     for (uint64_t off = 0; off < s.n; off += kSeg) {
       GradSeg d;
@@ -815,11 +836,6 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
       d.n = (uint32_t)(s.n - off < kSeg ? s.n - off : kSeg);
       d.vec = vec;
       segs.push_back(d);
-      // one launch covers every segment with kBlocksPerSeg waves, and a
-      // launch's work-items stay below 2^32
-      if (segs.size() > kMaxPlanSegs)
-        return fail(ARK_OPT_EINVAL, "too many elements (more than %llu segments of %u)",
-                    (unsigned long long)kMaxPlanSegs, kSeg);
     }
   }
   ark_grad_plan* p = new ark_grad_plan();

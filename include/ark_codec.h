@@ -46,7 +46,10 @@ int ark_hip_quant_f32_to_f16(const float *src, uint16_t *dst, uint64_t n,
 /* A batch of conversions run as one launch: the per-tensor loops of
  * training.rs:166-186 (dequantise every weight) and memory.rs:347-377
  * (sync_weights_to_gpu, quantise every weight).  The plan copies the span
- * table to the device once; each run converts every span. */
+ * table to the device once; each run converts every span.  No span's dst
+ * may share a byte with another span's dst or with any span's src (srcs may
+ * overlap each other): such a table is refused with ARK_OPT_EINVAL before
+ * any device call. */
 typedef struct ark_codec_span {
   const void *src; /* direction's source type, n elements */
   void *dst;       /* direction's destination type, n elements */

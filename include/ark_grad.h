@@ -38,7 +38,9 @@ typedef struct ark_grad_span {
 int ark_grad_accumulate(float *dst, const float *src, uint64_t n, void *stream);
 
 /* Every span of a model in one launch; the plan copies the span table to
- * the device once.  Spans must not overlap each other's dst. */
+ * the device once.  No span's dst may share a byte with another span's dst
+ * or with any span's src (srcs may overlap each other): such a table is
+ * refused with ARK_OPT_EINVAL before any device call. */
 typedef struct ark_grad_plan ark_grad_plan;
 int ark_grad_plan_create(const ark_grad_span *spans, int32_t n_spans, void *stream,
                          ark_grad_plan **out);

@@ -233,6 +233,55 @@ def test_next_rows_reject_bad_arguments_before_device_calls():
     assert L.ark_ckpt_probe(None, None, None, None, 0) == _abi.EINVAL
 
 
+def test_plans_reject_overlapping_spans_before_device_calls():
+    """A gradient or codec plan runs every span in one launch, so a dst that
+    shares a byte with another span's dst or src would race; such tables are
+    refused, naming both spans, before any device query (the addresses are
+    not memory at all).  Sources may overlap each other."""
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    h = C.c_void_p()
+
+    def grad(rows):
+        arr = (_abi.GradSpan * len(rows))()
+        for i, (d, s_, n) in enumerate(rows):
+            arr[i] = _abi.GradSpan(d, s_, n)
+        return L.ark_grad_plan_create(arr, len(rows), None, C.byref(h))
+
+    def codec(rows, direction=_abi.CODEC_F16_TO_F32):
+        arr = (_abi.CodecSpan * len(rows))()
+        for i, (s_, d, n) in enumerate(rows):
+            arr[i] = _abi.CodecSpan(s_, d, n)
+        return L.ark_codec_plan_create(arr, len(rows), direction, None, C.byref(h))
+
+    # gradient spans (dst, src, n), 4 B per element
+    bad = {
+        "same dst twice": [(1 * MB, 2 * MB, 1000), (1 * MB, 3 * MB, 1000)],
+        "dst inside another dst": [(1 * MB, 2 * MB, 1000), (1 * MB + 400, 3 * MB, 10)],
+        "dst on another span's src": [(1 * MB, 2 * MB, 1000), (2 * MB + 3996, 3 * MB, 10)],
+    }
+    for name, rows in bad.items():
+        assert grad(rows) == _abi.EINVAL and not h.value, name
+        assert "overlaps" in msg() and "span 0" in msg() and "span 1" in msg(), (name, msg())
+    # shared sources, touching spans and an empty span on top pass the check
+    for rows in ([(1 * MB, 3 * MB, 1000), (2 * MB, 3 * MB, 1000)],
+                 [(1 * MB, 3 * MB, 1000), (1 * MB + 4000, 4 * MB, 1000)],
+                 [(1 * MB, 3 * MB, 1000), (1 * MB, 1 * MB, 0)]):
+        assert grad(rows) != _abi.OK and "overlaps" not in msg(), msg()
+    # codec spans (src, dst, n): f16 -> f32 reads 2 B and writes 4 B per element
+    bad = {
+        "same dst twice": [(1 * MB, 2 * MB, 1000), (3 * MB, 2 * MB, 1000)],
+        "dst on another span's src": [(1 * MB, 2 * MB, 1000), (3 * MB, 1 * MB + 1996, 10)],
+        "dst partly over another dst": [(1 * MB, 2 * MB, 1000), (3 * MB, 2 * MB + 3996, 10)],
+    }
+    for name, rows in bad.items():
+        assert codec(rows) == _abi.EINVAL and not h.value, name
+        assert "overlaps" in msg() and "span 0" in msg() and "span 1" in msg(), (name, msg())
+    for rows in ([(1 * MB, 2 * MB, 1000), (1 * MB, 3 * MB, 1000)],
+                 [(1 * MB, 2 * MB, 1000), (3 * MB, 2 * MB + 4000, 1000)]):
+        assert codec(rows) != _abi.OK and "overlaps" not in msg(), msg()
+
+
 def test_missing_library_fails_loudly(tmp_path):
     """No fallback path: with the library absent, the loader and the entry
     points above it raise, naming the missing file (run in a fresh process so
