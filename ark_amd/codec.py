@@ -35,7 +35,9 @@ def quant_f32_to_f16(src, dst):
 
 class CodecPlan:
     """One launch converting every (src, dst) pair; direction is
-    ``"f16_to_f32"`` or ``"f32_to_f16"``.  The tensors must outlive the plan."""
+    ``"f16_to_f32"`` or ``"f32_to_f16"``.  No dst may share memory with
+    another pair's dst or src (the library refuses such pairs); sources may
+    be shared.  The tensors must outlive the plan."""
 
     def __init__(self, pairs, direction, stream=None):
         import torch

@@ -26,8 +26,9 @@ def accumulate(dst, src):
 
 
 class GradPlan:
-    """One launch doing dst += src for every (dst, src) pair.  The tensors
-    must outlive the plan."""
+    """One launch doing dst += src for every (dst, src) pair.  No dst may
+    share memory with another pair's dst or src (the library refuses such
+    pairs); sources may be shared.  The tensors must outlive the plan."""
 
     def __init__(self, pairs, stream=None):
         import torch
