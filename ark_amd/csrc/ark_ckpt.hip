@@ -422,19 +422,38 @@ struct Layout {
   uint64_t total = 0;  // end + trailer
 };
 
-int check_records(const ark_ckpt_record* r, int32_t n, bool need_device) {
+// Validates the record table.  One launch covers every record, so buffers a
+// call writes may share no byte with each other or with what it reads:
+// records_written (unpack, load) makes the records pairwise disjoint, and a
+// caller's image (pack writes it, unpack reads it) must be disjoint from
+// every record; records a call only reads may overlap each other.  These
+// address checks come before need_device's buffer queries.
+int check_records(const ark_ckpt_record* r, int32_t n, bool need_device,
+                  bool records_written = false, const void* image = nullptr,
+                  uint64_t image_bytes = 0) {
   if (n < 0 || (n > 0 && !r)) return fail(ARK_OPT_EINVAL, "record table is NULL or n < 0");
-  ark::BufferChecker checker;
+  std::vector<ark::Span> spans;
   for (int32_t i = 0; i < n; ++i) {
     if (r[i].dtype != ARK_CKPT_F16 && r[i].dtype != ARK_CKPT_F32)
       return fail(ARK_OPT_EINVAL, "record %d: dtype %u unknown", i, r[i].dtype);
     if (r[i].n > (1ull << 48)) return fail(ARK_OPT_EINVAL, "record %d: n too large", i);
     if (((uintptr_t)r[i].data) % esize(r[i].dtype))
       return fail(ARK_OPT_EINVAL, "record %d: data not aligned to its element", i);
-    if (need_device) {
-      int rc = checker.check(r[i].data, r[i].n * esize(r[i].dtype), "data", i);
-      if (rc) return rc;
-    }
+    const uintptr_t lo = (uintptr_t)r[i].data;
+    spans.push_back({lo, lo + r[i].n * esize(r[i].dtype), "data", i});
+  }
+  int rc;
+  if (records_written && (rc = ark::check_disjoint(spans, {}, "record", "the call"))) return rc;
+  if (image && image_bytes) {
+    const uintptr_t ilo = (uintptr_t)image, ihi = ilo + image_bytes;
+    for (const ark::Span& s : spans)
+      if (s.lo < s.hi && s.lo < ihi && ilo < s.hi)
+        return fail(ARK_OPT_EINVAL, "record %d data overlaps the image", s.idx);
+  }
+  if (need_device) {
+    ark::BufferChecker checker;
+    for (int32_t i = 0; i < n; ++i)
+      if ((rc = checker.check(r[i].data, r[i].n * esize(r[i].dtype), "data", i))) return rc;
   }
   return ARK_OPT_OK;
 }
@@ -826,7 +845,7 @@ int ark_ckpt_v4_image_bytes(const ark_ckpt_record* records, int32_t n, int with_
 int ark_ckpt_v4_pack(const ark_ckpt_record* records, int32_t n, uint64_t global_step,
                      uint64_t adam_step, const ark_opt_state* amp, void* image,
                      uint64_t image_bytes, void* stream) {
-  int rc = check_records(records, n, true);
+  int rc = check_records(records, n, true, false, image, image_bytes);
   if (rc) return rc;
   const Layout L = v4_layout(records, n, nullptr, amp != nullptr);
   if (image_bytes < L.total)
@@ -840,7 +859,7 @@ int ark_ckpt_v4_pack(const ark_ckpt_record* records, int32_t n, uint64_t global_
 
 int ark_ckpt_v4_unpack(const void* image, uint64_t image_bytes, const ark_ckpt_record* records,
                        int32_t n, const uint32_t* file_types, void* stream) {
-  int rc = check_records(records, n, true);
+  int rc = check_records(records, n, true, true, image, image_bytes);
   if (rc) return rc;
   if (n > 0 && !file_types) return fail(ARK_OPT_EINVAL, "file_types is NULL");
   for (int32_t i = 0; i < n; ++i)
@@ -1012,7 +1031,7 @@ int ark_ckpt_probe(const char* path, ark_ckpt_info* info, uint64_t* n_out, uint3
 int ark_ckpt_load(const char* path, const ark_ckpt_record* records, int32_t n,
                   ark_ckpt_info* info, ark_opt_state* amp, void* stream) {
   if (!path) return fail(ARK_OPT_EINVAL, "path is NULL");
-  int rc = check_records(records, n, true);
+  int rc = check_records(records, n, true, true);
   if (rc) return rc;
   Fd f;
   f.fd = ::open(path, O_RDONLY | O_CLOEXEC);

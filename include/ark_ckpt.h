@@ -99,7 +99,8 @@ int ark_ckpt_probe(const char *path, ark_ckpt_info *info, uint64_t *n_out,
                    uint32_t *type_out, int32_t max);
 
 /* CheckpointV3::load (io.rs:504-671) into device records: n_records must
- * equal the file's n_tensors and every record's n the file's n.  amp (may be
+ * equal the file's n_tensors and every record's n the file's n, and no two
+ * records may share a byte (all are written by one launch).  amp (may be
  * NULL) receives the trailer's state when info->has_amp. */
 int ark_ckpt_load(const char *path, const ark_ckpt_record *records, int32_t n_records,
                   ark_ckpt_info *info, ark_opt_state *amp, void *stream);
@@ -112,7 +113,9 @@ int ark_ckpt_load(const char *path, const ark_ckpt_record *records, int32_t n_re
  * ark_ckpt_v4_unpack: the inverse, from a V4 image in device memory laid out
  * as these records with the given file types would be; the file header and
  * every record header are checked on the device first.  Both return when
- * the stream has finished the work. */
+ * the stream has finished the work.  The image (image_bytes of it) may share
+ * no byte with any record, and unpack's records none with each other; such
+ * tables are refused with ARK_OPT_EINVAL before any device call. */
 int ark_ckpt_v4_image_bytes(const ark_ckpt_record *records, int32_t n_records,
                             int with_amp, uint64_t *bytes);
 int ark_ckpt_v4_pack(const ark_ckpt_record *records, int32_t n_records,

@@ -282,6 +282,41 @@ def test_plans_reject_overlapping_spans_before_device_calls():
         assert codec(rows) != _abi.OK and "overlaps" not in msg(), msg()
 
 
+def test_checkpoint_calls_reject_overlapping_buffers_before_device_calls():
+    """Unpack and load write every record in one launch, so their records
+    must be pairwise disjoint; pack writes the image and unpack reads it, so
+    the image must not overlap any record.  Refused before any device query
+    (the addresses are not memory); pack's records may overlap each other."""
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+
+    def recs(rows):
+        arr = (_abi.CkptRecord * len(rows))()
+        for i, (p, n, dt) in enumerate(rows):
+            arr[i] = _abi.CkptRecord(p, n, dt, 0)
+        return arr
+
+    F16, F32 = _abi.CKPT_F16, _abi.CKPT_F32
+    overlapping = recs([(1 * MB, 1000, F16), (1 * MB + 1000, 1000, F32)])
+    disjoint = recs([(1 * MB, 1000, F16), (2 * MB, 1000, F32)])
+    types = (C.c_uint32 * 2)(F16, F32)
+    # unpack: records written
+    assert L.ark_ckpt_v4_unpack(8 * MB, 1 * MB, overlapping, 2, types, None) == _abi.EINVAL
+    assert "record 0 data overlaps record 1 data" in msg(), msg()
+    assert L.ark_ckpt_v4_unpack(2 * MB - 16, 64, disjoint, 2, types, None) == _abi.EINVAL
+    assert "record 1 data overlaps the image" in msg(), msg()
+    assert L.ark_ckpt_v4_unpack(8 * MB, 1 * MB, disjoint, 2, types, None) != _abi.OK
+    assert "overlaps" not in msg(), msg()
+    # pack: the image written, records read (they may overlap each other)
+    assert L.ark_ckpt_v4_pack(disjoint, 2, 0, 0, None, 1 * MB + 512, 1 * MB, None) == _abi.EINVAL
+    assert "record 0 data overlaps the image" in msg(), msg()
+    assert L.ark_ckpt_v4_pack(overlapping, 2, 0, 0, None, 8 * MB, 1 * MB, None) != _abi.OK
+    assert "overlaps" not in msg(), msg()
+    # load: records written
+    assert L.ark_ckpt_load(b"/nonexistent", overlapping, 2, None, None, None) == _abi.EINVAL
+    assert "overlaps" in msg(), msg()
+
+
 def test_missing_library_fails_loudly(tmp_path):
     """No fallback path: with the library absent, the loader and the entry
     points above it raise, naming the missing file (run in a fresh process so

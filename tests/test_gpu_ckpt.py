@@ -379,11 +379,16 @@ def test_entry_points_reject_host_or_short_buffers(tmp_path):
     assert "buffer 1" in msg() and not os.path.exists(path), msg()
     image = torch.zeros(1 << 14, dtype=torch.uint8, device="cuda")
     recs[1] = _abi.CkptRecord(m.data_ptr(), 1 << 28, _abi.CKPT_F32, 0)  # 1 GiB from m
+    assert L.ark_ckpt_save_v4(os.fsencode(path), 1, 1, recs, 2, None, None) == _abi.EINVAL
+    assert "exceeds its allocation" in msg() and not os.path.exists(path), msg()
+    # pack and unpack refuse it too: as past its allocation, or, where the
+    # image lies inside that gigabyte, as overlapping the image
+    refused = lambda: "exceeds its allocation" in msg() or "overlaps the image" in msg()
     rc = L.ark_ckpt_v4_pack(recs, 2, 1, 1, None, image.data_ptr(), image.numel(), None)
-    assert rc == _abi.EINVAL and "exceeds its allocation" in msg(), msg()
+    assert rc == _abi.EINVAL and refused(), msg()
     types = (C.c_uint32 * 2)(_abi.CKPT_F16, _abi.CKPT_F32)
     rc = L.ark_ckpt_v4_unpack(image.data_ptr(), image.numel(), recs, 2, types, None)
-    assert rc == _abi.EINVAL and "exceeds its allocation" in msg(), msg()
+    assert rc == _abi.EINVAL and refused(), msg()
     recs[1] = _abi.CkptRecord(m.data_ptr(), 1000, _abi.CKPT_F32, 0)
     need = C.c_uint64()
     assert L.ark_ckpt_v4_image_bytes(recs, 2, 0, C.byref(need)) == 0
