@@ -60,6 +60,19 @@ def test_config2_eko237m_full_size_bit_exact():
     assert all(i.applied for i in infos) and infos[-1].state.t == 2
 
 
+def test_config2_full_size_at_a_scale_that_is_not_a_power_of_two():
+    """The same set at loss scale 49152 (1.5 x 2^15): the norm pass then
+    unscales each element before squaring instead of taking the squares from
+    the fp16 bits, over both its cache-allocating and its streaming blocks
+    (tables past ~134M elements have both).  Two steps, every element
+    compared."""
+    specs = config_tensors("c2")
+    sig = H.log_uniform_sigmas(len(specs), 20260503)
+    infos = _full_size_steps("c2", sig, 49152.0, 2, 20260503)
+    assert all(i.applied for i in infos) and infos[-1].state.t == 2
+    assert infos[-1].inv_scale == np.float32(1.0) / np.float32(49152.0)
+
+
 def test_config2_full_size_both_clip_branches():
     """BASELINE c2's sigma = 10^U(-5,-2) gives a global norm of about 35.8, so
     every c2 step clips.  The same 272-tensor set with those sigmas scaled to
