@@ -232,6 +232,45 @@ def test_accumulate_and_plan_eko237m():
     assert torch.equal(x, w)
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_plan_spans_at_random_alignments(case):
+    """Seeded plans of 1-40 spans, from empty through a few elements,
+    around one 4096-element segment and up to ~70k, each dst and src at its
+    own element offset (0-3, so 4-byte but mostly not 16-byte aligned: the
+    element path) in its own allocation, one source shared by two spans:
+    every result bit equal to torch's fp32 add, and a plain accumulation of
+    one such span too."""
+    torch = _torch()
+    rng = np.random.default_rng(500 + case)
+    g = torch.Generator(device="cuda").manual_seed(case)
+    pairs, want = [], []
+    shared = None
+    for _ in range(int(rng.integers(1, 41))):
+        r = rng.random()
+        n = (0 if r < 0.1 else int(rng.integers(1, 9)) if r < 0.3 else
+             int(rng.integers(4090, 4103)) if r < 0.5 else int(rng.integers(9, 70000)))
+        od, os_ = (int(x) for x in rng.integers(0, 4, 2))
+        d = torch.randn(n + 4, device="cuda", generator=g)[od:od + n]
+        if shared is not None and shared.numel() == n and rng.random() < 0.5:
+            src = shared
+        else:
+            src = torch.randn(n + 4, device="cuda", generator=g)[os_:os_ + n] * 1e-2
+            shared = src
+        want.append(d + src)
+        pairs.append((d, src))
+    plan = grad.GradPlan(pairs)
+    plan.run()
+    torch.cuda.synchronize()
+    for i, ((d, _), w) in enumerate(zip(pairs, want)):
+        assert torch.equal(d.view(torch.int32), w.view(torch.int32)), (case, i, d.numel())
+    plan.close()
+    d, src = pairs[-1]
+    w = d + src
+    grad.accumulate(d, src)
+    torch.cuda.synchronize()
+    assert torch.equal(d.view(torch.int32), w.view(torch.int32))
+
+
 @pytest.mark.parametrize("d_model,fused", [(64, False), (256, True), (64, True)])
 def test_handoff_into_optimizer_step(d_model, fused):
     """The backward tail on the device feeding ark_opt_step (fp32 grads):
