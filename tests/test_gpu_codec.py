@@ -135,6 +135,56 @@ def test_rejects_bad_buffers():
         check(lib().ark_hip_dequant_f16_to_f32(x.data_ptr(), x.data_ptr() + 4, 4, None))
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_plan_spans_at_random_alignments(case):
+    """Seeded codec plans of 1-40 spans, from empty through a few elements,
+    around one 4096-element segment and up to ~70k, each source and
+    destination at its own element offset inside its own allocation (so most
+    spans miss the 16-byte grid and take the element path), one source shared
+    by two spans; dequantise every fp16 pattern class, then quantise the
+    results back: both directions against the oracle's conversions bit for
+    bit."""
+    torch = _torch()
+    rng = np.random.default_rng(700 + case)
+    spans = []
+    for _ in range(int(rng.integers(1, 41))):
+        r = rng.random()
+        n = (0 if r < 0.1 else int(rng.integers(1, 9)) if r < 0.3 else
+             int(rng.integers(4090, 4103)) if r < 0.5 else int(rng.integers(9, 70000)))
+        spans.append((n, int(rng.integers(0, 8)), int(rng.integers(0, 4)), int(rng.integers(0, 8))))
+    bits, src, mid, back = [], [], [], []
+    shared = None
+    for n, os_, om, ob in spans:
+        if shared is not None and shared[0].size == n and rng.random() < 0.5:
+            h, s16 = shared
+        else:
+            h = rng.integers(0, 65536, n, dtype=np.uint32).astype(np.uint16)
+            base = torch.empty(n + 8, dtype=torch.int16, device="cuda")
+            base[os_:os_ + n] = torch.from_numpy(h.view(np.int16)).cuda()
+            s16 = base[os_:os_ + n].view(torch.float16)
+            shared = (h, s16)
+        bits.append(h)
+        src.append(s16)
+        mid.append(torch.empty(n + 4, dtype=torch.float32, device="cuda")[om:om + n])
+        back.append(torch.empty(n + 8, dtype=torch.float16, device="cuda")[ob:ob + n])
+    up = codec.CodecPlan(list(zip(src, mid)), "f16_to_f32")
+    up.run()
+    torch.cuda.synchronize()
+    for i, (h, d) in enumerate(zip(bits, mid)):
+        want = oracle.f16_to_f32(h) if h.size else np.zeros(0, np.float32)
+        assert np.array_equal(d.cpu().numpy().view(np.uint32), want.view(np.uint32)), (case, i)
+    up.close()
+    down = codec.CodecPlan(list(zip(mid, back)), "f32_to_f16")
+    down.run()
+    torch.cuda.synchronize()
+    for i, (d, b) in enumerate(zip(mid, back)):
+        f = d.cpu().numpy()
+        want = oracle.f32_to_f16(f) if f.size else np.zeros(0, np.uint16)
+        got = b.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got, want), (case, i)
+    down.close()
+
+
 def test_plans_over_thousands_of_tiny_spans():
     """2000 spans of 0-300 elements (empty ones skipped) in one codec plan
     and one accumulation plan, against the oracle's conversion and an fp32
