@@ -69,6 +69,10 @@ def _declare(L):
                               P, u64, P], C.c_int),
         "ark_ckpt_v4_unpack": ([P, u64, C.POINTER(_abi.CkptRecord), i32, C.POINTER(u32), P],
                                C.c_int),
+        "ark_ckpt_v4_pack_plan_create": ([C.POINTER(_abi.CkptRecord), i32, C.c_int, P, u64, P,
+                                          C.POINTER(H)], C.c_int),
+        "ark_ckpt_v4_pack_plan_run": ([H, u64, u64, C.POINTER(_abi.State)], C.c_int),
+        "ark_ckpt_plan_destroy": ([H], C.c_int),
         "ark_grad_accumulate": ([P, P, u64, P], C.c_int),
         "ark_grad_plan_create": ([C.POINTER(_abi.GradSpan), i32, P, C.POINTER(H)], C.c_int),
         "ark_grad_plan_run": ([H], C.c_int),

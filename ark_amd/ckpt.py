@@ -104,6 +104,42 @@ def pack(tensors, image, global_step, adam_step, amp_state=None):
                                  image.data_ptr(), image.numel(), _stream()))
 
 
+class PackPlan:
+    """Repeated V4 saves of the same tensors into the same uint8 GPU tensor
+    `image` (ark_ckpt_v4_pack_plan_*): the tables are uploaded once, and each
+    run queues the headers and data on the plan's stream without waiting.
+    with_amp: the image carries the AMP trailer, and every run passes the
+    state.  The tensors and the image must outlive the plan."""
+
+    def __init__(self, tensors, image, with_amp=False, stream=None):
+        import torch
+        self._recs = _records(tensors)
+        self._image = image
+        if stream is None:
+            stream = torch.cuda.current_stream()
+        self._stream = stream
+        h = C.c_void_p()
+        check(lib().ark_ckpt_v4_pack_plan_create(self._recs.arr, len(self._recs), int(with_amp),
+                                                 image.data_ptr(), image.numel(),
+                                                 C.c_void_p(stream.cuda_stream), C.byref(h)))
+        self._h = h
+
+    def run(self, global_step, adam_step, amp_state=None):
+        amp = C.byref(amp_state) if amp_state is not None else None
+        check(lib().ark_ckpt_v4_pack_plan_run(self._h, global_step, adam_step, amp))
+
+    def close(self):
+        if self._h:
+            check(lib().ark_ckpt_plan_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def unpack(image, tensors, file_types=None):
     """Scatter a V4 image (uint8 GPU tensor) into `tensors`; file_types
     defaults to each tensor's own type."""

@@ -88,6 +88,17 @@ static_assert(sizeof(ark_opt_state) == 32, "trailer holds a 32-byte state");
 
 inline uint64_t esize(uint32_t t) { return t == ARK_CKPT_F16 ? 2u : 4u; }
 
+// The bytes of a V4 image that change from one save of the same records to
+// the next: the file header (global step, Adam step, record count) and the
+// AMP trailer.  Passed to the header kernel by value, so a prepared table
+// (ark_ckpt_plan) needs no upload per save.
+constexpr uint32_t kDynBytes = (uint32_t)(kFileHeaderV4 + kTrailerBytes);
+struct DynHdr {
+  uint8_t bytes[kDynBytes];  // file header, then trailer
+  uint32_t has_trailer;
+  uint64_t trailer_off;  // image offset of the trailer
+};
+
 struct HdrPiece {  // up to 16 header bytes at an image offset
   uint64_t off;
   uint32_t len;
@@ -150,13 +161,23 @@ __device__ __forceinline__ u32x4 funnel16(const u32x4 a, const u32x4 b, uint32_t
 __device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return ld_g<uint8_t>(p); }
 __device__ __forceinline__ void st_u8(uint8_t* p, uint32_t v) { st_g<uint8_t>(p, (uint8_t)v); }
 
+// Threads [0, npieces) write the record headers from the uploaded pieces;
+// the next kDynBytes threads the file header and, when the image has one,
+// the trailer, from dyn.
 __global__ __launch_bounds__(kThreads) void header_kernel(const HdrPiece* __restrict__ pieces,
-                                                          uint32_t npieces,
+                                                          uint32_t npieces, DynHdr dyn,
                                                           uint8_t* __restrict__ img) {
   const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= npieces) return;
-  const HdrPiece p = pieces[i];
-  for (uint32_t b = 0; b < p.len; ++b) st_u8(img + p.off + b, p.bytes[b]);
+  if (i < npieces) {
+    const HdrPiece p = pieces[i];
+    for (uint32_t b = 0; b < p.len; ++b) st_u8(img + p.off + b, p.bytes[b]);
+    return;
+  }
+  const uint32_t j = i - npieces;
+  if (j < kFileHeaderV4)
+    st_u8(img + j, dyn.bytes[j]);
+  else if (j < kDynBytes && dyn.has_trailer)
+    st_u8(img + dyn.trailer_off + (j - kFileHeaderV4), dyn.bytes[j]);
 }
 
 // The tensor that block b belongs to (see PackRec).  hint[i] is the tensor
@@ -489,18 +510,22 @@ void le(uint8_t* dst, T v) {  // little endian, as the hosts this runs on
   memcpy(dst, &v, sizeof(T));
 }
 
-// Header pieces and data descriptors of a V4 image, uploaded, then both
-// kernels queued on stream and waited for.
-int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
-               const ark_opt_state* amp, uint8_t* img, hipStream_t stream) {
-  const Layout L = v4_layout(r, n, nullptr, amp != nullptr);
+// The device tables of a V4 pack, in one host buffer laid out for one
+// upload: the record-header pieces, the data descriptors, the block starts
+// and the hints.  What varies per save (file header, trailer) is not here.
+struct PackTables {
+  std::vector<uint8_t> host;
+  uint32_t npieces = 0;
+  size_t recs_off = 0, start_off = 0, hint_off = 0;
+  uint64_t blocks = 0;
+  uint64_t trailer_off = 0;  // first byte after the last record's data
+  int32_t n = 0;
+};
+
+int build_pack_tables(const ark_ckpt_record* r, int32_t n, PackTables& t) {
+  const Layout L = v4_layout(r, n, nullptr, false);
   std::vector<HdrPiece> pieces;
-  uint8_t fh[kFileHeaderV4];
-  le<uint32_t>(fh, ARK_CKPT_MAGIC_V4);
-  le<uint64_t>(fh + 4, gs);
-  le<uint64_t>(fh + 12, as);
-  le<uint64_t>(fh + 20, (uint64_t)n);
-  put_bytes(pieces, 0, fh, kFileHeaderV4);
+  pieces.reserve((size_t)n);
   std::vector<PackRec> recs((size_t)n);
   std::vector<uint32_t> start((size_t)n + 1);
   uint64_t blocks = 0;
@@ -524,48 +549,100 @@ int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
     if (blocks > 0x7FFFFFFFu) return fail(ARK_OPT_EINVAL, "image too large");
   }
   start[n] = (uint32_t)blocks;
-  if (amp) {
-    uint8_t tr[kTrailerBytes];
-    le<uint32_t>(tr, ARK_CKPT_MAGIC_AMP);
-    le<uint32_t>(tr + 4, kTrailerVersion);
-    memcpy(tr + 8, amp, sizeof(ark_opt_state));
-    put_bytes(pieces, L.end, tr, kTrailerBytes);
-  }
-  // one upload: header pieces | tensor table | block starts | hints
   const std::vector<uint32_t> hint =
       blocks ? make_hints(start, (uint32_t)n, blocks) : std::vector<uint32_t>();
   const size_t pb = pieces.size() * sizeof(HdrPiece), rb = recs.size() * sizeof(PackRec);
   const size_t stb = start.size() * sizeof(uint32_t), hb = hint.size() * sizeof(uint32_t);
-  std::vector<uint8_t> host(pb + rb + stb + hb);
-  memcpy(host.data(), pieces.data(), pb);
-  if (rb) memcpy(host.data() + pb, recs.data(), rb);
-  memcpy(host.data() + pb + rb, start.data(), stb);
-  if (hb) memcpy(host.data() + pb + rb + stb, hint.data(), hb);
-  StreamBuf d;
-  hipError_t e = d.alloc(host.size(), stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for checkpoint descriptors failed",
-                host.size());
+  t.host.resize(pb + rb + stb + hb);
+  if (pb) memcpy(t.host.data(), pieces.data(), pb);
+  if (rb) memcpy(t.host.data() + pb, recs.data(), rb);
+  memcpy(t.host.data() + pb + rb, start.data(), stb);
+  if (hb) memcpy(t.host.data() + pb + rb + stb, hint.data(), hb);
+  t.npieces = (uint32_t)pieces.size();
+  t.recs_off = pb;
+  t.start_off = pb + rb;
+  t.hint_off = pb + rb + stb;
+  t.blocks = blocks;
+  t.trailer_off = L.end;
+  t.n = n;
+  return ARK_OPT_OK;
+}
+
+DynHdr make_dyn(uint64_t gs, uint64_t as, int32_t n, const ark_opt_state* amp,
+                uint64_t trailer_off) {
+  DynHdr d{};
+  le<uint32_t>(d.bytes, ARK_CKPT_MAGIC_V4);
+  le<uint64_t>(d.bytes + 4, gs);
+  le<uint64_t>(d.bytes + 12, as);
+  le<uint64_t>(d.bytes + 20, (uint64_t)n);
+  if (amp) {
+    uint8_t* tr = d.bytes + kFileHeaderV4;
+    le<uint32_t>(tr, ARK_CKPT_MAGIC_AMP);
+    le<uint32_t>(tr + 4, kTrailerVersion);
+    memcpy(tr + 8, amp, sizeof(ark_opt_state));
+    d.has_trailer = 1u;
+    d.trailer_off = trailer_off;
   }
-  StreamSync sync{stream};
-  HdrPiece* dp = (HdrPiece*)d.p;
-  const PackRec* dr = (const PackRec*)((char*)d.p + pb);
-  const uint32_t* dst = (const uint32_t*)((char*)d.p + pb + rb);
-  const uint32_t* dhint = (const uint32_t*)((char*)d.p + pb + rb + stb);
-  ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, stream));
-  const uint32_t np = (uint32_t)pieces.size();
-  hipLaunchKernelGGL(header_kernel, dim3((np + kThreads - 1) / kThreads), dim3(kThreads), 0,
-                     stream, dp, np, img);
+  return d;
+}
+
+// Queues the header kernel and the data kernels of a pack whose tables sit
+// at dtab (device, laid out as PackTables::host).
+int launch_pack(const uint8_t* dtab, const PackTables& t, const DynHdr& dyn, uint8_t* img,
+                hipStream_t stream) {
+  const uint32_t nh = t.npieces + kDynBytes;
+  hipLaunchKernelGGL(header_kernel, dim3((nh + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                     stream, (const HdrPiece*)dtab, t.npieces, dyn, img);
   ARK_HIP(hipGetLastError());
   // a launch's work-items stay below 2^32: images past 64 GiB take several
   const uint64_t per_launch = launch_blocks(kPackMaxBlocks);
-  for (uint64_t b0 = 0; b0 < blocks; b0 += per_launch) {
-    const uint64_t nb = blocks - b0 < per_launch ? blocks - b0 : per_launch;
-    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)nb), dim3(kPackLanes), 0, stream, dr, dst,
-                       dhint, img, (uint32_t)b0);
+  for (uint64_t b0 = 0; b0 < t.blocks; b0 += per_launch) {
+    const uint64_t nb = t.blocks - b0 < per_launch ? t.blocks - b0 : per_launch;
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)nb), dim3(kPackLanes), 0, stream,
+                       (const PackRec*)(dtab + t.recs_off), (const uint32_t*)(dtab + t.start_off),
+                       (const uint32_t*)(dtab + t.hint_off), img, (uint32_t)b0);
     ARK_HIP(hipGetLastError());
   }
+  return ARK_OPT_OK;
+}
+
+// The arguments of a pack into image: the records, an image of at least the
+// V4 size (with the trailer when with_amp), 16-byte aligned device memory
+// that shares no byte with any record.
+int check_pack(const ark_ckpt_record* records, int32_t n, bool with_amp, const void* image,
+               uint64_t image_bytes) {
+  // the table and the image's size and alignment first, then the device
+  // queries of the records' buffers and the image
+  int rc = check_records(records, n, false, false, image, image_bytes);
+  if (rc) return rc;
+  const Layout L = v4_layout(records, n, nullptr, with_amp);
+  if (image_bytes < L.total)
+    return fail(ARK_OPT_EINVAL, "image holds %llu bytes, the checkpoint needs %llu",
+                (unsigned long long)image_bytes, (unsigned long long)L.total);
+  if ((uintptr_t)image & 15u) return fail(ARK_OPT_EINVAL, "image not 16-byte aligned");
+  if ((rc = check_records(records, n, true))) return rc;
+  return ark::check_buffer(image, L.total, "image", 0);
+}
+
+// The tables of a V4 image uploaded, both kernels queued on stream and
+// waited for.
+int pack_image(const ark_ckpt_record* r, int32_t n, uint64_t gs, uint64_t as,
+               const ark_opt_state* amp, uint8_t* img, hipStream_t stream) {
+  PackTables t;
+  int rc = build_pack_tables(r, n, t);
+  if (rc) return rc;
+  StreamBuf d;
+  hipError_t e = d.alloc(t.host.size(), stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for checkpoint descriptors failed",
+                t.host.size());
+  }
+  StreamSync sync{stream};
+  ARK_HIP(hipMemcpyAsync(d.p, t.host.data(), t.host.size(), hipMemcpyHostToDevice, stream));
+  if ((rc = launch_pack((const uint8_t*)d.p, t, make_dyn(gs, as, n, amp, t.trailer_off), img,
+                        stream)))
+    return rc;
   ARK_HIP(hipStreamSynchronize(stream));
   return ARK_OPT_OK;
 }
@@ -831,6 +908,16 @@ int parse_file(int fd, const char* path, Parsed* P) {
 
 }  // namespace
 
+// A pack prepared once: the tables on the device, the image and stream.
+struct ark_ckpt_plan {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  void* d_tables = nullptr;
+  uint8_t* image = nullptr;
+  bool with_amp = false;
+  PackTables t;  // sizes and offsets; its host copy is dropped after the upload
+};
+
 extern "C" {
 
 int ark_ckpt_v4_image_bytes(const ark_ckpt_record* records, int32_t n, int with_amp,
@@ -845,16 +932,66 @@ int ark_ckpt_v4_image_bytes(const ark_ckpt_record* records, int32_t n, int with_
 int ark_ckpt_v4_pack(const ark_ckpt_record* records, int32_t n, uint64_t global_step,
                      uint64_t adam_step, const ark_opt_state* amp, void* image,
                      uint64_t image_bytes, void* stream) {
-  int rc = check_records(records, n, true, false, image, image_bytes);
+  const int rc = check_pack(records, n, amp != nullptr, image, image_bytes);
   if (rc) return rc;
-  const Layout L = v4_layout(records, n, nullptr, amp != nullptr);
-  if (image_bytes < L.total)
-    return fail(ARK_OPT_EINVAL, "image holds %llu bytes, the checkpoint needs %llu",
-                (unsigned long long)image_bytes, (unsigned long long)L.total);
-  if ((uintptr_t)image & 15u) return fail(ARK_OPT_EINVAL, "image not 16-byte aligned");
-  if ((rc = ark::check_buffer(image, L.total, "image", 0))) return rc;
   return pack_image(records, n, global_step, adam_step, amp, (uint8_t*)image,
                     (hipStream_t)stream);
+}
+
+int ark_ckpt_v4_pack_plan_create(const ark_ckpt_record* records, int32_t n, int with_amp,
+                                 void* image, uint64_t image_bytes, void* stream,
+                                 ark_ckpt_plan** out) {
+  if (!out) return fail(ARK_OPT_EINVAL, "out is NULL");
+  *out = nullptr;
+  int rc = check_pack(records, n, with_amp != 0, image, image_bytes);
+  if (rc) return rc;
+  ark_ckpt_plan* p = new ark_ckpt_plan();
+  if ((rc = build_pack_tables(records, n, p->t))) {
+    delete p;
+    return rc;
+  }
+  p->stream = (hipStream_t)stream;
+  p->image = (uint8_t*)image;
+  p->with_amp = with_amp != 0;
+  hipError_t e = hipGetDevice(&p->device);
+  if (e == hipSuccess) e = hipMalloc(&p->d_tables, p->t.host.size());
+  if (e == hipSuccess)
+    e = hipMemcpy(p->d_tables, p->t.host.data(), p->t.host.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (p->d_tables) (void)hipFree(p->d_tables);
+    delete p;
+    return ark::hip_fail(e, "ark_ckpt_v4_pack_plan_create");
+  }
+  p->t.host.clear();
+  p->t.host.shrink_to_fit();
+  *out = p;
+  return ARK_OPT_OK;
+}
+
+int ark_ckpt_v4_pack_plan_run(ark_ckpt_plan* p, uint64_t global_step, uint64_t adam_step,
+                              const ark_opt_state* amp) {
+  if (!p) return fail(ARK_OPT_EINVAL, "plan is NULL");
+  if ((amp != nullptr) != p->with_amp)
+    return fail(ARK_OPT_EINVAL, p->with_amp ? "the plan's image has a trailer: amp is NULL"
+                                            : "the plan's image has no trailer: amp must be NULL");
+  ark::DeviceGuard g(p->device);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
+  return launch_pack((const uint8_t*)p->d_tables, p->t,
+                     make_dyn(global_step, adam_step, p->t.n, amp, p->t.trailer_off), p->image,
+                     p->stream);
+}
+
+int ark_ckpt_plan_destroy(ark_ckpt_plan* p) {
+  if (!p) return ARK_OPT_OK;
+  int rc = ARK_OPT_OK;
+  if (p->d_tables) {
+    ark::DeviceGuard g(p->device);
+    hipError_t e = hipFree(p->d_tables);
+    if (e != hipSuccess) rc = ark::hip_fail(e, "hipFree");
+  }
+  delete p;
+  return rc;
 }
 
 int ark_ckpt_v4_unpack(const void* image, uint64_t image_bytes, const ark_ckpt_record* records,

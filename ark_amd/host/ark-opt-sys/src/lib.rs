@@ -224,6 +224,22 @@ extern "C" {
     pub fn ark_ckpt_v4_unpack(image: *const c_void, image_bytes: u64,
                               records: *const ark_ckpt_record, n_records: i32,
                               file_types: *const u32, stream: *mut c_void) -> c_int;
+    /// A pack prepared once for repeated saves of the same records into the
+    /// same device image (the trainer's periodic checkpoint,
+    /// `src/training.rs:483-604`); each run is queued without waiting.
+    pub fn ark_ckpt_v4_pack_plan_create(records: *const ark_ckpt_record, n_records: i32,
+                                        with_amp: c_int, image: *mut c_void, image_bytes: u64,
+                                        stream: *mut c_void,
+                                        out: *mut *mut ark_ckpt_plan) -> c_int;
+    pub fn ark_ckpt_v4_pack_plan_run(plan: *mut ark_ckpt_plan, global_step: u64, adam_step: u64,
+                                     amp: *const ark_opt_state) -> c_int;
+    pub fn ark_ckpt_plan_destroy(plan: *mut ark_ckpt_plan) -> c_int;
+}
+
+/// Opaque checkpoint pack plan.
+#[repr(C)]
+pub struct ark_ckpt_plan {
+    _private: [u8; 0],
 }
 
 // ---- include/ark_grad.h ------------------------------------------------------

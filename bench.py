@@ -535,6 +535,20 @@ def run_ckpt(a):
         torch.cuda.synchronize()
         res[name] = dict(ms=e0.elapsed_time(e1) / steps,
                          wall_ms=(time.perf_counter() - t0) * 1e3 / steps)
+    # the same pack from a prepared plan: runs queued back to back, so the
+    # events time the device work (header kernel + data kernel) without the
+    # per-call table upload and host wait
+    plan = ckpt.PackPlan(recs, img)
+    for _ in range(min(a.warmup, 5)):
+        plan.run(1000, 999)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        plan.run(1000, 999)
+    e1.record()
+    torch.cuda.synchronize()
+    res["plan"] = dict(ms=e0.elapsed_time(e1) / steps)
+    plan.close()
     d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
     path = os.path.join(d, f"ark_bench_ckpt_{os.getpid()}.bin")
     try:
@@ -561,15 +575,22 @@ def run_ckpt(a):
         cpu = dict(value=round(2 * nbytes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
                    sample=f"{reps} V4 images of embed + layer 0 ({nbytes // reps} B each) built "
                           f"by the oracle writer in {el:.1f} s")
-    pk = 2 * nb / (res["pack"]["ms"] * 1e-3) / 1e9
+    pk = 2 * nb / (res["plan"]["ms"] * 1e-3) / 1e9
+    pk_call = 2 * nb / (res["pack"]["ms"] * 1e-3) / 1e9
     up = 2 * nb / (res["unpack"]["ms"] * 1e-3) / 1e9
     out = {
         "metric": "EKO-237M checkpoint V4 pack from device buffers, GB/s of HBM traffic (1 GPU)",
         "value": round(pk, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
-        "warmup": min(a.warmup, 5), "ms_per_step": round(res["pack"]["ms"], 4),
+        "warmup": min(a.warmup, 5), "ms_per_step": round(res["plan"]["ms"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
         "data": "synthetic",
         "config": {"workload": "ckpt: EKO-237M V4 image, 816 records", "image_bytes": nb,
+                   "timing": "value and ms_per_step: pack-plan runs queued back to back "
+                             "(ark_ckpt_v4_pack_plan_run, header + data kernels, HIP events); "
+                             "pack_call_* and unpack_*: one ark_ckpt_v4_pack / "
+                             "ark_ckpt_v4_unpack call each (table upload, kernels, host wait)",
+                   "pack_call_ms": round(res["pack"]["ms"], 4),
+                   "pack_call_GBs": round(pk_call, 2),
                    "unpack_ms": round(res["unpack"]["ms"], 4), "unpack_GBs": round(up, 2),
                    "pack_call_wall_ms": round(res["pack"]["wall_ms"], 3),
                    "save_file_s": round(save_s, 3), "save_file_GBs": round(nb / save_s / 1e9, 2),

@@ -126,6 +126,27 @@ int ark_ckpt_v4_unpack(const void *image, uint64_t image_bytes,
                        const ark_ckpt_record *records, int32_t n_records,
                        const uint32_t *file_types, void *stream);
 
+/* A pack prepared once for repeated saves of the same records into the same
+ * device image: the trainer's checkpoint every N steps (training.rs:483-604,
+ * CheckpointV3::save_fp16 at io.rs:432-502) kept in device memory, or staged
+ * there for a copy that overlaps the next steps.  Create checks the
+ * arguments as ark_ckpt_v4_pack does (with_amp: the image carries the
+ * trailer) and uploads the record headers and data descriptors once.  Each
+ * run queues the headers and the data on the plan's stream and returns
+ * without waiting: the file header's steps and the trailer's state (amp,
+ * required exactly when with_amp) are taken at the call, by value.  The
+ * image is the same bytes ark_ckpt_v4_pack writes.  The records and the
+ * image must stay allocated while runs are queued; destroy frees the plan's
+ * device tables. */
+typedef struct ark_ckpt_plan ark_ckpt_plan;
+
+int ark_ckpt_v4_pack_plan_create(const ark_ckpt_record *records, int32_t n_records,
+                                 int with_amp, void *image, uint64_t image_bytes,
+                                 void *stream, ark_ckpt_plan **out);
+int ark_ckpt_v4_pack_plan_run(ark_ckpt_plan *plan, uint64_t global_step,
+                              uint64_t adam_step, const ark_opt_state *amp);
+int ark_ckpt_plan_destroy(ark_ckpt_plan *plan);
+
 #ifdef __cplusplus
 }
 #endif

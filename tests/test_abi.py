@@ -317,6 +317,39 @@ def test_checkpoint_calls_reject_overlapping_buffers_before_device_calls():
     assert "overlaps" in msg(), msg()
 
 
+def test_pack_plan_rejects_bad_arguments_before_device_calls():
+    """The pack plan checks its arguments as ark_ckpt_v4_pack does (the
+    image's size with or without the trailer, its alignment, overlap with a
+    record) before any device query, and its run refuses a NULL plan and an
+    AMP state that does not match the plan (the addresses are not memory)."""
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    arr = (_abi.CkptRecord * 2)()
+    arr[0] = _abi.CkptRecord(1 * MB, 1000, _abi.CKPT_F16, 0)
+    arr[1] = _abi.CkptRecord(2 * MB, 1000, _abi.CKPT_F32, 0)
+    size = 28 + 16 + 2000 + 16 + 4000
+    h = C.c_void_p(12345)
+    assert L.ark_ckpt_v4_pack_plan_create(arr, 2, 0, 8 * MB, size, None, None) == _abi.EINVAL
+    assert "out is NULL" in msg(), msg()
+    assert L.ark_ckpt_v4_pack_plan_create(arr, 2, 0, 8 * MB, size - 1, None,
+                                          C.byref(h)) == _abi.EINVAL
+    assert "needs %d" % size in msg() and h.value is None, msg()
+    assert L.ark_ckpt_v4_pack_plan_create(arr, 2, 1, 8 * MB, size, None,
+                                          C.byref(h)) == _abi.EINVAL
+    assert "needs %d" % (size + 40) in msg(), msg()
+    assert L.ark_ckpt_v4_pack_plan_create(arr, 2, 0, 8 * MB + 8, size, None,
+                                          C.byref(h)) == _abi.EINVAL
+    assert "16-byte aligned" in msg(), msg()
+    assert L.ark_ckpt_v4_pack_plan_create(arr, 2, 0, 1 * MB + 512, size, None,
+                                          C.byref(h)) == _abi.EINVAL
+    assert "record 0 data overlaps the image" in msg(), msg()
+    assert L.ark_ckpt_v4_pack_plan_create(None, 2, 0, 8 * MB, size, None,
+                                          C.byref(h)) == _abi.EINVAL
+    assert L.ark_ckpt_v4_pack_plan_run(None, 0, 0, None) == _abi.EINVAL
+    assert "plan is NULL" in msg(), msg()
+    assert L.ark_ckpt_plan_destroy(None) == _abi.OK
+
+
 def test_missing_library_fails_loudly(tmp_path):
     """No fallback path: with the library absent, the loader and the entry
     points above it raise, naming the missing file (run in a fresh process so

@@ -365,6 +365,132 @@ def test_random_tables_at_random_buffer_alignments(case):
         np.testing.assert_array_equal(x, y, err_msg=f"case {case} record {i}")
 
 
+def _state(t, scale, skipped):
+    return _abi.State(t=t, loss_scale=scale, clean_steps=t % 7, consecutive_nonfinite=t % 3,
+                      skipped_steps=skipped, early_stop=0)
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_pack_plan_runs_write_the_oracle_bytes(case):
+    """A pack plan over a seeded random table (buffers at random element
+    offsets, as above) run several times with new steps, new AMP states and
+    new buffer contents in between: after each run the image equals the
+    oracle writer's bytes for that save (with the 40-byte trailer when the
+    plan carries one), and ark_ckpt_v4_pack's image of the same save."""
+    torch = _torch()
+    rng = np.random.default_rng(7000 + case)
+    nrec = int(rng.integers(1, 40))
+    with_amp = case % 2 == 1
+    src = []
+    for _ in range(nrec):
+        r = rng.random()
+        n = 0 if r < 0.1 else int(rng.integers(1, 9)) if r < 0.35 else int(rng.integers(9, 30000))
+        dt = torch.float16 if rng.random() < 0.5 else torch.float32
+        off = int(rng.integers(0, 8))
+        src.append(torch.empty(n + 8, dtype=dt, device="cuda")[off:off + n])
+    nb = ckpt.image_bytes(src, with_amp)
+    img = torch.empty(nb + 64, dtype=torch.uint8, device="cuda")[16 * int(rng.integers(0, 4)):][:nb]
+    ref = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    plan = ckpt.PackPlan(src, img, with_amp=with_amp)
+    try:
+        for k in range(3):
+            _fill_random(src, 300 + 10 * case + k)
+            amp = _state(5 * k + case, 2.0 ** (k + 3), 11 * k) if with_amp else None
+            gs, ad = 1000 * case + k, 999 * case + 2 * k
+            img.fill_(0xAB)
+            plan.run(gs, ad, amp)
+            torch.cuda.synchronize()
+            want = K.write_v4(gs, ad, [_bits(t) if t.numel() else
+                                       np.zeros(0, np.uint16 if t.element_size() == 2
+                                                else np.float32) for t in src])
+            if with_amp:
+                want += K.amp_trailer(bytes(amp))
+            assert img.cpu().numpy().tobytes() == want, (case, k)
+            ckpt.pack(src, ref, gs, ad, amp)
+            assert torch.equal(img, ref), (case, k)
+    finally:
+        plan.close()
+
+
+def test_pack_plan_full_eko237m_and_split_launches(monkeypatch):
+    """The plan over the 816-record EKO-237M table writes the image the
+    one-call pack writes (2.37 GB, the oracle's bytes in test_full_eko237m_image),
+    with its data split over many launches too (ARK_CKPT_LAUNCH_BLOCKS is read
+    at each run)."""
+    torch = _torch()
+    ps = _params(EKO_237M, 5)
+    tens = ckpt.param_tensors(ps)
+    nb = ckpt.image_bytes(tens, True)
+    ref = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    img = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    amp = _state(4000, 65536.0, 3)
+    ckpt.pack(tens, ref, 4001, 4000, amp)
+    plan = ckpt.PackPlan(tens, img, with_amp=True)
+    try:
+        img.zero_()
+        plan.run(4001, 4000, amp)
+        torch.cuda.synchronize()
+        assert torch.equal(img, ref)
+        monkeypatch.setenv("ARK_CKPT_LAUNCH_BLOCKS", "4099")
+        img.zero_()
+        plan.run(4001, 4000, amp)
+        torch.cuda.synchronize()
+        assert torch.equal(img, ref)
+    finally:
+        plan.close()
+
+
+def test_pack_plan_in_a_hip_graph():
+    """A plan run captured in a HIP graph (header and data kernels, no
+    memset node) and replayed several times, with the buffers changed and
+    the image cleared eagerly between replays: every replay writes the bytes
+    of an eager pack of the buffers at that moment (the steps and state are
+    the captured ones)."""
+    torch = _torch()
+    ps = _params(ODD, 6)
+    tens = ckpt.param_tensors(ps)
+    nb = ckpt.image_bytes(tens, True)
+    img = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    ref = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    amp = _state(12, 1024.0, 1)
+    stream = torch.cuda.Stream()
+    plan = ckpt.PackPlan(tens, img, with_amp=True, stream=stream)
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            plan.run(13, 12, amp)
+        for k in range(4):
+            _fill_random(tens, 60 + k)
+            img.fill_(k)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            ckpt.pack(tens, ref, 13, 12, amp)
+            assert torch.equal(img, ref), k
+        del graph
+    finally:
+        plan.close()
+
+
+def test_pack_plan_refuses_a_state_that_does_not_match():
+    torch = _torch()
+    ps = _params(ODD, 7)
+    tens = ckpt.param_tensors(ps)
+    img = torch.empty(ckpt.image_bytes(tens, True), dtype=torch.uint8, device="cuda")
+    with_t = ckpt.PackPlan(tens, img, with_amp=True)
+    without = ckpt.PackPlan(tens, img[:ckpt.image_bytes(tens)], with_amp=False)
+    try:
+        with pytest.raises(ArkOptError, match="amp is NULL"):
+            with_t.run(1, 1)
+        with pytest.raises(ArkOptError, match="amp must be NULL"):
+            without.run(1, 1, _state(1, 1.0, 0))
+    finally:
+        with_t.close()
+        without.close()
+    with pytest.raises(ArkOptError, match="the checkpoint needs"):
+        ckpt.PackPlan(tens, img[:ckpt.image_bytes(tens)], with_amp=True)
+
+
 def test_rejects_bad_files(tmp_path):
     torch = _torch()
     x = [torch.zeros(5, dtype=torch.float16, device="cuda"),
