@@ -8,7 +8,9 @@ tensors on the GPU and writes the same V4 file byte for byte;
 buffers given in file order.  ``save_params`` / ``load_params`` do the same
 for a ParamSet and its Optimizer, in the tensor order of
 Trainer::guardar_checkpoint (training.rs:536-604), with the loss-scaler
-state carried in the trailer the reference's loader skips.
+state carried in the trailer the reference's loader skips.  ``PackPlan``
+repeats the device half of a save (the V4 image in device memory) with the
+tables uploaded once and no host wait per save.
 """
 import ctypes as C
 import os
