@@ -135,9 +135,10 @@ int ark_ckpt_v4_unpack(const void *image, uint64_t image_bytes,
  * run queues the headers and the data on the plan's stream and returns
  * without waiting: the file header's steps and the trailer's state (amp,
  * required exactly when with_amp) are taken at the call, by value.  The
- * image is the same bytes ark_ckpt_v4_pack writes.  The records and the
- * image must stay allocated while runs are queued; destroy frees the plan's
- * device tables. */
+ * image is the same bytes ark_ckpt_v4_pack writes.  A run captured in a HIP
+ * graph replays the steps and state it was captured with.  The records and
+ * the image must stay allocated while runs are queued; destroy frees the
+ * plan's device tables. */
 typedef struct ark_ckpt_plan ark_ckpt_plan;
 
 int ark_ckpt_v4_pack_plan_create(const ark_ckpt_record *records, int32_t n_records,
