@@ -386,14 +386,15 @@ __global__ __launch_bounds__(kThreads) void check_kernel(const CheckDesc* __rest
 
 // ---- host side --------------------------------------------------------------
 
+// The file image of a save or load (the descriptor tables take StreamBuf,
+// stream-ordered allocations with no device-wide synchronisation on free).
 struct DevBuf {
   void* p = nullptr;
   ~DevBuf() {
     if (p) (void)hipFree(p);
   }
 };
-// Stream-ordered allocation from the device's default memory pool (no
-// device-wide synchronisation on free), for the small descriptor tables.
+
 // hint[i] = the tensor holding block min(i << kHintShift, blocks - 1), for
 // i = 0 .. ceil(blocks / 2^kHintShift): the last r with start[r] <= that
 // block, as find_rec defines it.  blocks >= 1.
@@ -1012,18 +1013,21 @@ int ark_ckpt_v4_unpack(const void* image, uint64_t image_bytes, const ark_ckpt_r
   // header check on the device
   std::vector<CheckDesc> cd((size_t)n);
   for (int32_t i = 0; i < n; ++i) cd[i] = CheckDesc{L.hdr[i], records[i].n, file_types[i], 0};
-  DevBuf d;
+  // one upload: the header descriptors, then the failure index (all ones:
+  // no failure)
   const size_t cb = cd.size() * sizeof(CheckDesc);
-  hipError_t e = hipMalloc(&d.p, cb + 16);
+  std::vector<uint8_t> host(cb + 16, 0xFF);
+  if (cb) memcpy(host.data(), cd.data(), cb);
+  StreamBuf d;
+  hipError_t e = d.alloc(host.size(), s);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    return fail(ARK_OPT_ENOMEM, "hipMalloc(%zu) failed", cb + 16);
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for checkpoint descriptors failed",
+                host.size());
   }
   StreamSync sync{s};
   uint32_t* dbad = (uint32_t*)((char*)d.p + cb);
-  const uint32_t init = 0xFFFFFFFFu;
-  if (cb) ARK_HIP(hipMemcpyAsync(d.p, cd.data(), cb, hipMemcpyHostToDevice, s));
-  ARK_HIP(hipMemcpyAsync(dbad, &init, 4, hipMemcpyHostToDevice, s));
+  ARK_HIP(hipMemcpyAsync(d.p, host.data(), host.size(), hipMemcpyHostToDevice, s));
   hipLaunchKernelGGL(check_kernel, dim3((uint32_t)(n + 1 + kThreads - 1) / kThreads),
                      dim3(kThreads), 0, s, (const CheckDesc*)d.p, (uint32_t)n,
                      (const uint8_t*)image, dbad);
