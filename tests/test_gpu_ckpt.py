@@ -472,6 +472,24 @@ def test_pack_plan_in_a_hip_graph():
         plan.close()
 
 
+@pytest.mark.parametrize("with_amp", [False, True])
+def test_pack_plan_of_an_empty_table(with_amp):
+    """No records: a run writes the file header (and the trailer) only."""
+    torch = _torch()
+    nb = ckpt.image_bytes([], with_amp)
+    assert nb == 28 + (40 if with_amp else 0)
+    img = torch.full((nb,), 0xAB, dtype=torch.uint8, device="cuda")
+    plan = ckpt.PackPlan([], img, with_amp=with_amp)
+    try:
+        amp = _state(3, 8.0, 2) if with_amp else None
+        plan.run(21, 20, amp)
+        torch.cuda.synchronize()
+        want = K.write_v4(21, 20, []) + (K.amp_trailer(bytes(amp)) if with_amp else b"")
+        assert img.cpu().numpy().tobytes() == want
+    finally:
+        plan.close()
+
+
 def test_pack_plan_refuses_a_state_that_does_not_match():
     torch = _torch()
     ps = _params(ODD, 7)
