@@ -162,22 +162,28 @@ __device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return ld_g<uint8_
 __device__ __forceinline__ void st_u8(uint8_t* p, uint32_t v) { st_g<uint8_t>(p, (uint8_t)v); }
 
 // Threads [0, npieces) write the record headers from the uploaded pieces;
-// the next kDynBytes threads the file header and, when the image has one,
-// the trailer, from dyn.
+// thread npieces the file header and, when the image has one, the trailer,
+// from dyn (unrolled, so every byte is read from the kernel arguments at a
+// fixed offset).
 __global__ __launch_bounds__(kThreads) void header_kernel(const HdrPiece* __restrict__ pieces,
                                                           uint32_t npieces, DynHdr dyn,
                                                           uint8_t* __restrict__ img) {
   const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
   if (i < npieces) {
-    const HdrPiece p = pieces[i];
-    for (uint32_t b = 0; b < p.len; ++b) st_u8(img + p.off + b, p.bytes[b]);
+    const HdrPiece* p = pieces + i;
+    const uint64_t off = p->off;
+    const uint32_t len = p->len;
+    for (uint32_t b = 0; b < len; ++b) st_u8(img + off + b, ld_u8(p->bytes + b));
     return;
   }
-  const uint32_t j = i - npieces;
-  if (j < kFileHeaderV4)
-    st_u8(img + j, dyn.bytes[j]);
-  else if (j < kDynBytes && dyn.has_trailer)
-    st_u8(img + dyn.trailer_off + (j - kFileHeaderV4), dyn.bytes[j]);
+  if (i != npieces) return;
+#pragma unroll
+  for (uint32_t j = 0; j < kFileHeaderV4; ++j) st_u8(img + j, dyn.bytes[j]);
+  if (dyn.has_trailer) {
+#pragma unroll
+    for (uint32_t j = 0; j < kTrailerBytes; ++j)
+      st_u8(img + dyn.trailer_off + j, dyn.bytes[kFileHeaderV4 + j]);
+  }
 }
 
 // The tensor that block b belongs to (see PackRec).  hint[i] is the tensor
@@ -591,7 +597,7 @@ DynHdr make_dyn(uint64_t gs, uint64_t as, int32_t n, const ark_opt_state* amp,
 // at dtab (device, laid out as PackTables::host).
 int launch_pack(const uint8_t* dtab, const PackTables& t, const DynHdr& dyn, uint8_t* img,
                 hipStream_t stream) {
-  const uint32_t nh = t.npieces + kDynBytes;
+  const uint32_t nh = t.npieces + 1;
   hipLaunchKernelGGL(header_kernel, dim3((nh + kThreads - 1) / kThreads), dim3(kThreads), 0,
                      stream, (const HdrPiece*)dtab, t.npieces, dyn, img);
   ARK_HIP(hipGetLastError());
