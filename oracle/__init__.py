@@ -79,6 +79,8 @@ def lib():
     L.ark_ref_opt_step.argtypes = [C.POINTER(_abi.Tensor), C.c_int32, C.POINTER(_abi.HParams),
                                    C.POINTER(_abi.State), C.c_float, C.c_int,
                                    C.POINTER(_abi.StepInfo)]
+    L.ark_ref_finalize.argtypes = [C.POINTER(_abi.HParams), C.POINTER(_abi.State), C.c_double,
+                                   C.c_int, C.c_float, C.POINTER(_abi.StepInfo)]
     L.ark_ref_apply_given.argtypes = [C.POINTER(_abi.Tensor), C.c_int32, C.POINTER(_abi.HParams),
                                       C.c_uint32, C.c_float, C.POINTER(_abi.StepInfo), C.c_int]
     L.ark_ref_record_overflow.argtypes = [C.POINTER(_abi.HParams), C.POINTER(_abi.State),
@@ -261,6 +263,16 @@ class Optimizer:
         info = _abi.StepInfo()
         st = lib().ark_ref_record_overflow(C.byref(self.hp), C.byref(self.state), C.byref(info))
         return st, info
+
+
+def finalize(hp, state, sumsq, nonfinite, lr):
+    """The scalar half of a step (ark_ref_finalize): skip / clip / t /
+    loss-scale decisions from a given canonical sum of squares and
+    non-finite flag; `state` is updated in place.  Returns (status, info)."""
+    info = _abi.StepInfo()
+    st = lib().ark_ref_finalize(C.byref(hp), C.byref(state), sumsq, 1 if nonfinite else 0, lr,
+                                C.byref(info))
+    return st, info
 
 
 def amp_replay(hp, state, events):

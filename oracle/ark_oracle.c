@@ -664,9 +664,9 @@ int ark_ref_amp_replay(const ark_opt_hparams *hp, ark_opt_state *st,
   return status;
 }
 
-int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
-                     const ark_opt_hparams *hp, ark_opt_state *st, float lr,
-                     int nthreads, ark_opt_step_info *info) {
+int ark_ref_finalize(const ark_opt_hparams *hp, ark_opt_state *st,
+                     double sumsq, int nonfinite, float lr,
+                     ark_opt_step_info *info) {
   if (st->early_stop) {
     fill_info(info, st, 0, 0, 0, ARK_OPT_EARLY_STOP, 0.0, 0.0f, 1.0f,
               1.0f / st->loss_scale, lr, 0.0f);
@@ -674,9 +674,6 @@ int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
   }
   float scale = st->loss_scale;
   float inv = 1.0f / scale; /* training.rs:244, before any state change */
-  int32_t nonfinite = 0;
-  double sumsq =
-      ark_ref_sumsq(tab, nt, hp->grad_dtype, inv, nthreads, &nonfinite);
   if (nonfinite) { /* training.rs:293-305: no update, t unchanged */
     /* the sum of a non-finite step is reported as NaN */
     int status = amp_skip(hp, st);
@@ -689,11 +686,29 @@ int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
   st->t += 1;                                            /* optimizer.rs:172 */
   ark_ref_scalars s0;
   ark_ref_prologue(lr, hp->beta1, hp->beta2, 0.0f, st->t, &s0);
-  run_update(tab, nt, hp, st->t, lr, inv, clipped, coef, nthreads);
   amp_clean(hp, st, scale); /* training.rs:316-326 */
   fill_info(info, st, 1, 0, clipped, ARK_OPT_OK, sumsq, norm, coef, inv, lr,
             s0.lr_eff);
   return ARK_OPT_OK;
+}
+
+int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
+                     const ark_opt_hparams *hp, ark_opt_state *st, float lr,
+                     int nthreads, ark_opt_step_info *info) {
+  ark_opt_step_info f;
+  int32_t nonfinite = 0;
+  double sumsq = 0.0;
+  if (!st->early_stop) /* the sum is over grads unscaled by the step's scale */
+    sumsq = ark_ref_sumsq(tab, nt, hp->grad_dtype, 1.0f / st->loss_scale,
+                          nthreads, &nonfinite);
+  int status = ark_ref_finalize(hp, st, sumsq, nonfinite, lr, &f);
+  /* the update runs with the advanced t (optimizer.rs:172 comes first); the
+   * scale bookkeeping inside the finalize does not touch what it reads */
+  if (f.applied)
+    run_update(tab, nt, hp, st->t, lr, f.inv_scale, f.clipped, f.clip_coef,
+               nthreads);
+  if (info) *info = f;
+  return status;
 }
 
 int ark_ref_apply_given(const ark_opt_tensor *tab, int32_t nt,

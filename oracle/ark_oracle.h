@@ -95,6 +95,15 @@ int ark_ref_opt_step(const ark_opt_tensor *tab, int32_t nt,
                      const ark_opt_hparams *hp, ark_opt_state *st, float lr,
                      int nthreads, ark_opt_step_info *info);
 
+/* The scalar half of ark_ref_opt_step: given the step's canonical sum of
+ * squares and non-finite flag (ark_ref_sumsq at inv_scale = 1/loss_scale of
+ * the state on entry), the skip / clip / t / loss-scale decisions and the
+ * step info, with the state machine on *st; no element is touched.
+ * ark_ref_opt_step is ark_ref_sumsq + this + the element update. */
+int ark_ref_finalize(const ark_opt_hparams *hp, ark_opt_state *st,
+                     double sumsq, int nonfinite, float lr,
+                     ark_opt_step_info *info);
+
 /* Same as ark_ref_opt_step but with the global scalars taken from `given`
  * (applied, clipped, clip_coef, inv_scale, lr_eff from another
  * implementation's step info) instead of recomputed: the elementwise update

@@ -100,48 +100,138 @@ def test_config4_scaleup_full_size_bit_exact():
     assert infos[0].applied == 1
 
 
-def test_config3_amp_stress_trajectory_5000_steps():
-    """EKO-237M, 5000 steps from scale 65536 (cap 2^24); on ~0.1 % of steps
-    (seeded) +inf, -inf or NaN at 1-16 seeded positions of random tensors.
-    Skip decisions, loss scale, t and counters must follow the oracle's
-    state machine at every step."""
+def _c3_poke_plan(specs, steps, seed):
+    """The c3 injection schedule: on ~0.1 % of steps (seeded) plus the fixed
+    steps 1500, 1501 (two in a row) and 2100 (mid-recovery), +inf, -inf or
+    NaN at 1-16 seeded positions of seeded tensors.  {step: [(tensor,
+    position, fp16 bits)]}."""
+    rng = np.random.default_rng(seed)
+    bad = np.union1d(np.nonzero(rng.random(steps) < 0.001)[0], [1500, 1501, 2100])
+    specials = (0x7C00, 0xFC00, 0x7E00)
+    plan = {}
+    for k in bad.tolist():
+        plan[k] = []
+        for _ in range(int(rng.integers(1, 17))):
+            ti = int(rng.integers(len(specs)))
+            plan[k].append((ti, int(rng.integers(specs[ti].n)), specials[int(rng.integers(3))]))
+    return plan
+
+
+def _c3_sample(specs, ts, seed):
+    """The elements the c3 test follows through every step: every element
+    of gamma_final, of every g1 and g2, and of one seeded 768 x 768 tensor;
+    a seeded strided sample of the embedding (~1.07M) and of every layer's
+    w2 (~38k each, ~1.15M in all).  [(tensor index, element indices)] and
+    the matching oracle HostTensors (their own copies, from `ts`)."""
+    rng = np.random.default_rng(seed)
+    names = [s.name for s in specs]
+    square = [i for i, s in enumerate(specs) if s.name.endswith((".wq", ".wk", ".wv", ".wo"))]
+    picks = [(names.index("gamma_final"), None), (int(rng.choice(square)), None)]
+    picks += [(i, None) for i, s in enumerate(specs) if s.name.endswith((".g1", ".g2"))]
+    picks.append((names.index("embed"), 23))
+    picks += [(i, 41) for i, s in enumerate(specs) if s.name.endswith(".w2")]
+    sample, host = [], []
+    for i, stride in picks:
+        idx = (np.arange(specs[i].n, dtype=np.int64) if stride is None else
+               np.arange(int(rng.integers(stride)), specs[i].n, stride, dtype=np.int64))
+        t = ts[i]
+        sample.append((i, idx))
+        host.append(oracle.HostTensor(t.w[idx].copy(), t.g[idx].copy(), t.m[idx].copy(),
+                                      t.v[idx].copy(), t.weight_decay, t.flags))
+    return sample, host
+
+
+def test_config3_amp_stress_5000_steps_scalars_and_elements():
+    """EKO-237M, 5000 steps from scale 65536 (cap 2^24), gradients fixed from
+    step 0, with the seeded injections of _c3_poke_plan (five random events
+    at this seed, plus the three fixed ones).  Every step's scalars -- skip
+    decision, canonical sum of squares, norm, clip coefficient, inv_scale,
+    lr_eff, t, loss scale and counters -- are checked bit for bit against
+    the oracle's own: its sum of squares over the host copy of the
+    gradients once per distinct loss scale, its finite check over the
+    poked tensors, its state machine (ark_ref_finalize).  The oracle then
+    runs the elementwise update of every applied step, with its own
+    scalars, over the elements of _c3_sample, and after step 5000 those
+    w/m/v elements on the device must equal its bits.  The oracle side runs
+    on a host thread while the device steps."""
+    import threading
     import torch
     specs = config_tensors("c3")
-    sig = H.log_uniform_sigmas(len(specs), 3)
-    ps = H.gpu_problem(specs, 3, HP["weight_decay"], sig, 65536.0)
+    steps, seed, lr = 5000, 3, HP["lr"]
+    sig = H.log_uniform_sigmas(len(specs), seed)
+    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, 65536.0)
     cfg, opt = _opt(ps, 65536.0)
-    rng = np.random.default_rng(2026)
-    steps = 5000
-    bad_steps = np.nonzero(rng.random(steps) < 0.001)[0]
-    bad_steps = np.union1d(bad_steps, [1500, 1501, 2100])  # consecutive and mid-growth cases
-    specials = np.array([0x7C00, 0xFC00, 0x7E00], np.uint16).view(np.int16)
-    ref_state = _abi.State()
-    oracle.lib().ark_ref_state_init(opt.hp, ref_state)
+    plan = _c3_poke_plan(specs, steps, 2156)
+    assert sorted(plan) == [15, 287, 813, 1500, 1501, 2100, 2778, 4993]
+    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, 65536.0, nthreads=THREADS)
+    sample, host = _c3_sample(specs, ts, 31)
+    assert sum(idx.size for _, idx in sample) > 2_800_000
+    ref_info = [None] * steps
+    failure = []
+
+    def oracle_side():
+        try:
+            st = _abi.State()
+            oracle.lib().ark_ref_state_init(opt.hp, st)
+            sums = {}
+            sub = oracle.Optimizer(host, opt.hp, nthreads=THREADS)
+            for k in range(steps):
+                if k in plan:
+                    hit = sorted({ti for ti, _, _ in plan[k]})
+                    poked = [ts[ti].copy() for ti in hit]
+                    for ti, pos, bits in plan[k]:
+                        poked[hit.index(ti)].g[pos] = bits
+                    sq, bad = oracle.sumsq(poked, _abi.GRAD_F16, 1.0, nthreads=THREADS)
+                    assert bad, k
+                else:
+                    scale = float(st.loss_scale)
+                    if scale not in sums:
+                        inv = np.float32(1.0) / np.float32(scale)
+                        sums[scale] = oracle.sumsq(ts, _abi.GRAD_F16, inv, nthreads=THREADS)
+                    sq, bad = sums[scale]
+                    assert not bad, k
+                _, ri = oracle.finalize(opt.hp, st, sq, bad, lr)
+                if ri.applied:
+                    sub.apply_given(lr, st.t, ri)
+                ref_info[k] = ri
+        except BaseException as e:  # reported on the main thread
+            failure.append(e)
+
+    worker = threading.Thread(target=oracle_side)
+    worker.start()
     g16 = [ps.g(i).view(torch.int16) for i in range(len(specs))]
-    events = np.zeros(steps, bool)
-    scales = []
+    dev_info = []
     for k in range(steps):
-        poked = []
-        if k in bad_steps:
-            events[k] = True
-            for _ in range(int(rng.integers(1, 17))):
-                ti = int(rng.integers(len(specs)))
-                pos = int(rng.integers(specs[ti].n))
-                poked.append((ti, pos, int(g16[ti][pos].item())))
-                g16[ti][pos] = int(specials[rng.integers(3)])
-        rc, gi = opt.step_all(cfg.lr, info=True)
-        rrc, _ = oracle.amp_replay(opt.hp, ref_state, events[k:k + 1])
-        assert rc == rrc and gi.applied == (not events[k]), k
-        assert gi.state.as_dict() == ref_state.as_dict(), (k, gi.state.as_dict())
-        for ti, pos, old in reversed(poked):
+        undo = []
+        for ti, pos, bits in plan.get(k, ()):
+            undo.append((ti, pos, int(g16[ti][pos].item())))
+            g16[ti][pos] = int(np.array(bits, np.uint16).view(np.int16))
+        _, gi = opt.step_all(lr, info=True)
+        dev_info.append(gi)
+        for ti, pos, old in reversed(undo):
             g16[ti][pos] = old
-        scales.append(gi.state.loss_scale)
-    # seeded schedule: skips at 1500, 1501, 2100 and 2717 halve 65536 down to
-    # 4096; 2000 clean steps later it doubles back to 8192
-    assert bad_steps.tolist() == [1500, 1501, 2100, 2717]
-    assert ref_state.t == steps - 4 and ref_state.skipped_steps == 4
-    assert min(scales) == 4096.0 and scales[-1] == 8192.0
-    assert scales.index(8192.0, 2717) == 2717 + 2000
+    worker.join()
+    assert not failure, failure
+    for k in range(steps):
+        d = H.info_matches(dev_info[k], ref_info[k])
+        assert not d, (k, d)
+        assert dev_info[k].applied == (k not in plan), k
+    scales = [i.state.loss_scale for i in dev_info]
+    last = dev_info[-1].state
+    assert last.t == steps - 8 and last.skipped_steps == 8
+    # 65536 halved by the seven skips up to 2778 to 512; 2000 clean steps
+    # later (4778) it doubles to 1024; the skip at 4993 halves it again
+    assert min(scales) == 512.0 and scales[4777] == 512.0 and scales[4778] == 1024.0
+    assert scales[-1] == 512.0
+    assert all(i.clipped for i in dev_info if i.applied)
+    for (i, idx), h in zip(sample, host):
+        at = torch.from_numpy(idx).cuda()
+        w = H.to_host(ps.w(i)[at])
+        m = H.to_host(ps.m(i)[at])
+        v = H.to_host(ps.v(i)[at])
+        assert not H.bits_differ16(w, h.w).any(), (specs[i].name, "w")
+        assert not H.bits_differ32(m, h.m).any(), (specs[i].name, "m")
+        assert not H.bits_differ32(v, h.v).any(), (specs[i].name, "v")
     opt.close()
 
 

@@ -95,3 +95,50 @@ def test_clipped_step_equals_unclipped_step_on_clipped_gradients():
     assert np.array_equal(a.w, b.w)
     assert np.array_equal(a.m.view(np.uint32), b.m.view(np.uint32))
     assert np.array_equal(a.v.view(np.uint32), b.v.view(np.uint32))
+
+
+def test_finalize_then_elementwise_update_is_the_step():
+    """ark_ref_finalize (the step's scalars from a given sum of squares) and
+    ark_ref_apply_given (the elementwise update from those scalars) together
+    reproduce ark_ref_opt_step: 60 steps over three tensors with clipped,
+    unclipped and non-finite steps, loss-scale growth, and an early stop.
+    The full-size AMP stress test checks the device's scalars with this
+    split, the sum taken once per distinct loss scale."""
+    from oracle import harness as H
+    rng = np.random.default_rng(41)
+    sizes = [3000, 257, 64]
+    hp = _hp(1.0, scale=2.0 ** 12)
+    hp.scale_up_every = 7
+    hp.max_consecutive_nonfinite = 3
+    mk = lambda: [oracle.HostTensor((rng.standard_normal(n) * 0.02).astype(np.float16)
+                                    .view(np.uint16), np.zeros(n, np.uint16),
+                                    np.zeros(n, np.float32), np.zeros(n, np.float32),
+                                    0.1 if k else 0.0) for k, n in enumerate(sizes)]
+    a = mk()
+    b = [t.copy() for t in a]
+    ra = oracle.Optimizer(a, hp)
+    st = _abi.State()
+    oracle.lib().ark_ref_state_init(hp, st)
+    bad_at = {5, 6, 20, 40, 41, 42, 43}  # 40-43: four in a row, past the limit of 3
+    seen = set()
+    for k in range(60):
+        sig = float(10.0 ** rng.uniform(-4, -1)) * hp.loss_scale_init
+        for ta, tb in zip(a, b):
+            ta.g[:] = (rng.standard_normal(ta.n) * sig).astype(np.float16).view(np.uint16)
+            if k in bad_at:
+                ta.g[int(rng.integers(ta.n))] = 0x7E00
+            tb.g[:] = ta.g
+        sa, ia = ra.step(3e-4)
+        inv = np.float32(1.0) / np.float32(st.loss_scale)
+        sq, bad = oracle.sumsq(b, _abi.GRAD_F16, inv) if not st.early_stop else (0.0, False)
+        sb, ib = oracle.finalize(hp, st, sq, bad, 3e-4)
+        oracle.Optimizer(b, hp).apply_given(3e-4, st.t, ib)
+        assert sa == sb and not H.info_matches(ia, ib), (k, H.info_matches(ia, ib))
+        seen.add((ia.applied, ia.clipped, sa))
+        for ta, tb in zip(a, b):
+            assert np.array_equal(ta.w, tb.w) and np.array_equal(ta.m.view(np.uint32),
+                                                                  tb.m.view(np.uint32))
+            assert np.array_equal(ta.v.view(np.uint32), tb.v.view(np.uint32))
+    assert ra.state.early_stop == 1 and ra.state.skipped_steps == 7
+    # applied clipped and unclipped, skipped, and stopped steps all occurred
+    assert {(1, 1, 0), (1, 0, 0), (0, 0, 0), (0, 0, _abi.EARLY_STOP)} <= seen, seen
