@@ -677,6 +677,16 @@ int unpack_image(const uint8_t* img, uint64_t img_bytes, const ark_ckpt_record* 
   }
   start[n] = (uint32_t)blocks;
   if (blocks == 0) return ARK_OPT_OK;
+  {
+    // a record's buffer may be an optimizer's gradient
+    std::vector<const void*> dst((size_t)n);
+    std::vector<uint64_t> bytes((size_t)n);
+    for (int32_t i = 0; i < n; ++i) {
+      dst[i] = r[i].data;
+      bytes[i] = r[i].n * (r[i].dtype == ARK_CKPT_F16 ? 2u : 4u);
+    }
+    ark::opt_units_invalidate(dst.data(), bytes.data(), (size_t)n);
+  }
   const std::vector<uint32_t> hint = make_hints(start, (uint32_t)n, blocks);
   const size_t rb = recs.size() * sizeof(UnpackRec), stb = start.size() * sizeof(uint32_t);
   const size_t hb = hint.size() * sizeof(uint32_t);
@@ -725,19 +735,28 @@ void sync_parent_dir(const char* path) {
 
 std::atomic<uint64_t> g_tmp_counter{0};
 
-// The file a save to path replaces: path itself, or the file a symbolic
-// link at path resolves to.
+// The file a save to path writes: path itself, or, when path is a symbolic
+// link, what the chain of links names, resolved one link at a time as
+// open(2) resolves it, so that a dangling link names the file to create (as
+// File::create creates it, io.rs:450).  Relative link targets are taken from
+// the directory of the link.  A chain of more than 40 links is left to fail
+// at the open, as open(2) fails on it.
 std::string save_target(const char* path) {
-  struct stat st;
-  if (lstat(path, &st) == 0 && S_ISLNK(st.st_mode)) {
-    char* r = realpath(path, nullptr);
-    if (r) {
-      std::string t(r);
-      free(r);
-      return t;
+  std::string p(path);
+  for (int hops = 0; hops < 40; ++hops) {
+    struct stat st;
+    if (lstat(p.c_str(), &st) != 0 || !S_ISLNK(st.st_mode)) return p;
+    std::vector<char> buf((size_t)(st.st_size > 0 ? st.st_size : PATH_MAX) + 1);
+    const ssize_t k = readlink(p.c_str(), buf.data(), buf.size() - 1);
+    if (k < 0) return p;
+    std::string link(buf.data(), (size_t)k);
+    if (!link.empty() && link[0] != '/') {
+      const size_t slash = p.rfind('/');
+      if (slash != std::string::npos) link = p.substr(0, slash + 1) + link;
     }
+    p = link;
   }
-  return std::string(path);
+  return p;
 }
 
 int read_exact(int fd, void* buf, uint64_t len, uint64_t off, const char* path) {
@@ -1090,15 +1109,19 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
   // checkpoint intact.  The temporary name is unique to this call
   // (<target>.tmp.<pid>.<n>, created with O_EXCL), so concurrent saves and a
   // user's own files never share it.  A symbolic link at path is followed, as
-  // File::create follows it (io.rs:450): the link stays and its target
-  // becomes the new file (a dangling link is replaced by the file).
+  // File::create follows it (io.rs:450): the link stays and the file it names
+  // becomes the new file, also when the link dangles.  A new file gets mode
+  // 0666 less the umask, File::create's; a file it replaces hands its mode,
+  // and where permitted its owner and group, on to the new one, which
+  // File::create keeps by truncating in place.  Other names (hard links) of a
+  // replaced file keep the old contents: a rename cannot carry them over.
   const std::string target = save_target(path);
   std::string tmp;
   Fd f;
   for (int attempt = 0; attempt < 16 && f.fd < 0; ++attempt) {
     tmp = target + ".tmp." + std::to_string((long)getpid()) + "." +
           std::to_string(g_tmp_counter.fetch_add(1));
-    f.fd = ::open(tmp.c_str(), O_RDWR | O_CREAT | O_EXCL | O_CLOEXEC, 0644);
+    f.fd = ::open(tmp.c_str(), O_RDWR | O_CREAT | O_EXCL | O_CLOEXEC, 0666);
     if (f.fd < 0 && errno != EEXIST) break;
   }
   if (f.fd < 0) return io_fail("create", tmp.c_str());
@@ -1109,6 +1132,15 @@ int ark_ckpt_save_v4(const char* path, uint64_t global_step, uint64_t adam_step,
       if (!done) (void)::unlink(name.c_str());
     }
   } tmp_file{tmp};
+  {
+    struct stat old;
+    if (::stat(target.c_str(), &old) == 0 && S_ISREG(old.st_mode)) {
+      struct stat cur;
+      if (fstat(f.fd, &cur) == 0 && (cur.st_uid != old.st_uid || cur.st_gid != old.st_gid))
+        (void)fchown(f.fd, old.st_uid, old.st_gid);  // EPERM for others' files: kept ours
+      if (fchmod(f.fd, old.st_mode & 07777) != 0) return io_fail("set the mode of", tmp.c_str());
+    }
+  }
   // Preferred: reserve the whole file, map it, and copy each chunk into the
   // mapping from several threads (writes to one file through write() are
   // serialised by the file's lock).  The reservation makes a full disk fail

@@ -146,6 +146,10 @@ int run_flat(const void* src, void* dst, uint64_t n, void* stream) {
   if ((rc = ark::check_buffer(src, sb, "src", 0))) return rc;
   if ((rc = ark::check_buffer(dst, db, "dst", 0))) return rc;
   if (overlaps(src, sb, dst, db)) return ark::fail(ARK_OPT_EINVAL, "src and dst overlap");
+  {
+    const void* d = dst;
+    ark::opt_units_invalidate(&d, &db, 1);  // dst may be an optimizer's gradient
+  }
   const uint32_t vec = ((((uintptr_t)src | (uintptr_t)dst) & 15u) == 0) ? 1u : 0u;
   uint64_t blocks = (n + Shape<DIR>::kSpan - 1) / Shape<DIR>::kSpan;
   if (blocks > kMaxFlatBlocks) blocks = kMaxFlatBlocks;
@@ -163,6 +167,8 @@ struct ark_codec_plan {
   uint32_t direction = 0;
   uint32_t nseg = 0;
   CodecSeg* d_segs = nullptr;
+  std::vector<const void*> span_dst;  // what a run writes, for
+  std::vector<uint64_t> span_bytes;   // ark::opt_units_invalidate
 };
 
 extern "C" {
@@ -233,6 +239,10 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
   p->stream = (hipStream_t)stream;
   p->direction = direction;
   p->nseg = (uint32_t)segs.size();
+  for (int32_t i = 0; i < n_spans; ++i) {
+    p->span_dst.push_back(spans[i].dst);
+    p->span_bytes.push_back(spans[i].n * ds);
+  }
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess && !segs.empty()) {
     e = hipMalloc(&p->d_segs, segs.size() * sizeof(CodecSeg));
@@ -251,6 +261,7 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
 int ark_codec_plan_run(ark_codec_plan* p) {
   if (!p) return ark::fail(ARK_OPT_EINVAL, "plan is NULL");
   if (p->nseg == 0) return ARK_OPT_OK;
+  ark::opt_units_invalidate(p->span_dst.data(), p->span_bytes.data(), p->span_dst.size());
   ark::DeviceGuard g(p->device);
   if (!g.ok) return ark::fail(ARK_OPT_EHIP, "cannot select device %d", p->device);
   if (p->direction == ARK_CODEC_F16_TO_F32) {

@@ -91,6 +91,22 @@ int lds_per_cu(int device);
 // cannot tell.
 uint32_t resident_lds_bytes(const void* kernel, int threads, int blocks);
 
+// Every library call that writes device memory a caller passed in reports
+// the byte ranges it is about to write: every optimizer handle whose norm
+// units are fresh (written by the gradient hand-off's final calls for its
+// next step) and whose gradients overlap one of them loses those units, so
+// its next step reads the gradients.  Host-only; cheap when no handle is
+// fresh (ark_opt.hip).
+void opt_units_invalidate(const void* const* dst, const uint64_t* bytes, size_t count);
+
+// Sets device dev up for ark_grad_embed_scatter_noalloc (ark_grad.hip): looks
+// up the address of that device's copy of the static workspace and creates the
+// event that orders the calls, once per device.  The library's set-up calls
+// (ark_opt_create, ark_grad_plan_create) run it, so that a later
+// no-allocation call, also one under graph capture, needs no runtime lookup.
+// Repeated calls return at once.
+int grad_scratch_prepare(int dev);
+
 // Scratch device memory from the stream-ordered pool, freed in stream order
 // when the owner goes out of scope (after the work queued on it).
 struct StreamBuf {

@@ -715,42 +715,69 @@ int scatter_launch(float* embed_grad, uint32_t vocab, uint32_t d, const uint32_t
 }  // namespace
 
 // ---- the scatter's workspace without allocation --------------------------
-// One file-scope device array per GPU, held from the library's first use on
-// that GPU to the end of the process.  Host code never passes `scratch`
-// itself to a kernel (on the host the name is only a stand-in for the
-// symbol): it looks the array's device address up once per device with
-// hipGetSymbolAddress, with that device current, and uses that address.
+// One file-scope device array.  It is part of this library's code object, so
+// every GPU the library is used on holds a copy from the code object's load
+// there (the library's first kernel launch or symbol lookup on that GPU) to
+// the end of the process.  Host code never passes `scratch` itself to a
+// kernel (on the host the name is only a stand-in for the symbol): it looks
+// the array's device address up once per device with hipGetSymbolAddress,
+// with that device current, and uses that address.
 static __device__ __align__(256) uint8_t scratch[ARK_GRAD_SCRATCH_BYTES];
 
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
 
-// The address of device dev's copy of scratch, looked up on the first call
-// for that device.
-int scratch_ptr(int dev, void** out) {
-  *out = nullptr;
-  if (dev < 0 || dev >= kMaxDevices)
-    return fail(ARK_OPT_EINVAL, "device %d out of range for the static scratch", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    ark::DeviceGuard g(dev);
-    if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", dev);
+// Per device: the address of its copy of scratch, and an event recorded on
+// the stream of each eager no-allocation call after its last launch, which
+// the next eager call waits for, so calls from different streams or threads
+// take the array in turn.
+struct ScratchSlot {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
+std::mutex g_scratch_mu;  // guards g_scratch and orders the calls' enqueues
+ScratchSlot g_scratch[kMaxDevices];
+
+// Sets device dev's slot up; the caller holds g_scratch_mu.
+int scratch_setup_locked(int dev) {
+  ScratchSlot& S = g_scratch[dev];
+  if (S.ptr && S.done) return ARK_OPT_OK;
+  ark::DeviceGuard g(dev);
+  if (!g.ok) return fail(ARK_OPT_EHIP, "cannot select device %d", dev);
+  if (!S.ptr) {
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr) {
       (void)hipGetLastError();
       return ark::hip_fail(e, "hipGetSymbolAddress(scratch)");
     }
-    g_scratch_ptr[dev] = p;
+    S.ptr = p;
   }
-  *out = g_scratch_ptr[dev];
+  if (!S.done) {
+    hipError_t e = hipEventCreateWithFlags(&S.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      S.done = nullptr;
+      (void)hipGetLastError();
+      return ark::hip_fail(e, "hipEventCreateWithFlags for the static scratch");
+    }
+  }
   return ARK_OPT_OK;
 }
 
 }  // namespace
+
+namespace ark {
+
+int grad_scratch_prepare(int dev) {
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ARK_OPT_EINVAL, "device %d out of range for the static scratch", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return scratch_setup_locked(dev);
+}
+
+}  // namespace ark
 
 struct ark_grad_plan {
   int device = 0;
@@ -848,6 +875,9 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
   }
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess) {
+    // the no-allocation scatter's set-up on this device (best effort, as in
+    // ark_opt_create)
+    (void)ark::grad_scratch_prepare(p->device);
     // ARK_GRAD_BLOCKS_PER_CU=8..32 overrides the cap, 0 lifts it (a tuning
     // knob: results do not depend on it)
     int per_cu = kPlanBlocksPerCu;
@@ -992,10 +1022,39 @@ int ark_grad_embed_scatter_noalloc(float* embed_grad, uint32_t vocab, uint32_t d
     (void)hipGetLastError();
     return ark::hip_fail(e, "device of the stream");
   }
-  void* ws = nullptr;
-  if ((rc = scratch_ptr(dev, &ws))) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ARK_OPT_EINVAL, "device %d out of range for the static scratch", dev);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return ark::hip_fail(e, "hipStreamIsCapturing");
+  }
+  const bool captured = cap != hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot& S = g_scratch[dev];
+  if (!S.ptr || !S.done) {
+    // the one-time lookup may load the code object; it is no stream work
+    // and cannot be captured
+    if (captured)
+      return fail(ARK_OPT_EINVAL,
+                  "the static scratch of device %d is not set up yet and the stream is "
+                  "capturing: make one ark_grad_embed_scatter_noalloc call, or create an "
+                  "optimizer handle or a gradient plan, on that device before capturing",
+                  dev);
+    if ((rc = scratch_setup_locked(dev))) return rc;
+  }
   invalidate_embed_units(embed_grad, vocab, d);
-  return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)ws, L, s);
+  if (captured)  // a graph node: its replays are ordered by the caller
+    return scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)S.ptr, L, s);
+  if (S.recorded) ARK_HIP(hipStreamWaitEvent(s, S.done, 0));
+  rc = scatter_launch(embed_grad, vocab, d, tokens, dx0, batch_seq, (char*)S.ptr, L, s);
+  // recorded even after a failed launch, which may have queued part of its work
+  e = hipEventRecord(S.done, s);
+  if (e == hipSuccess) S.recorded = true;
+  if (rc) return rc;
+  if (e != hipSuccess) return ark::hip_fail(e, "hipEventRecord for the static scratch");
+  return ARK_OPT_OK;
 }
 
 }  // extern "C"

@@ -278,6 +278,9 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
 
   int dev = 0;
   ARK_HIP(hipGetDevice(&dev));
+  // set-up of the no-allocation scatter on this device, so that its first
+  // call may come under graph capture (best effort: that call retries it)
+  (void)ark::grad_scratch_prepare(dev);
   ark::BufferChecker checker;
   for (int32_t i = 0; i < n_tensors; ++i) {
     const ark_opt_tensor& t = tensors[i];
@@ -545,6 +548,11 @@ int ark_hip_adam_step(float* w, const float* g, float* m, float* v, uint64_t n, 
   if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
   if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;
   if ((rc = check_buffer(v, n * 4u, "v", 0))) return rc;
+  {
+    const void* d[3] = {w, m, v};  // any may be another handle's gradient
+    const uint64_t b[3] = {n * 4u, n * 4u, n * 4u};
+    ark::opt_units_invalidate(d, b, 3);
+  }
   const bool vec = (((uw | ug | um | uv) & 15u) == 0);
   StepScalars sc{};
   sc.applied = 1u;
@@ -577,6 +585,11 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   if ((rc = check_buffer(g, n * 4u, "g", 0))) return rc;
   if ((rc = check_buffer(m, n * 4u, "m", 0))) return rc;
   if ((rc = check_buffer(v, n * 4u, "v", 0))) return rc;
+  {
+    const void* d[3] = {w, m, v};  // any may be another handle's gradient
+    const uint64_t b[3] = {n * 2u, n * 4u, n * 4u};
+    ark::opt_units_invalidate(d, b, 3);
+  }
   const bool vec =
       ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15u) == 0);
   StepScalars sc{};

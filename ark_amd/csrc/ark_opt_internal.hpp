@@ -50,10 +50,7 @@ int opt_units_for_tensor(ark_opt_handle* h, const void* g, uint64_t n, bool requ
 // Marks h's units as written for its next step (fresh) or not.
 void opt_units_set_fresh(ark_opt_handle* h, bool fresh);
 
-// The library's other gradient writers report the byte ranges they are
-// about to write: every handle with fresh units whose gradients overlap one
-// of them loses those units, so its next step reads the gradients.
-void opt_units_invalidate(const void* const* dst, const uint64_t* bytes, size_t count);
+// (opt_units_invalidate, the other writers' side, is in ark_common.hpp.)
 
 // units -> one partial per norm block of spb segments, exactly what
 // sumsq_kernel would write for the same gradients (launch_sumsq's part_sum).

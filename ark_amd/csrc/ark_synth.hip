@@ -123,6 +123,9 @@ uint32_t grid_for(uint64_t n) {
 
 int status(hipError_t e) { return e == hipSuccess ? 0 : -2; }
 
+// What a call is about to write may be an optimizer's gradient.
+void written(const void* p, uint64_t bytes) { ark::opt_units_invalidate(&p, &bytes, 1); }
+
 }  // namespace
 
 extern "C" {
@@ -132,6 +135,7 @@ int ark_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed,
                          void* stream) {
   if (n == 0) return 0;
   if (!out) return -1;
+  written(out, n * 2u);
   hipLaunchKernelGGL(normal_kernel<true>, dim3(grid_for(n)), dim3(256), 0,
                      (hipStream_t)stream, (void*)out, n,
                      synth_base(seed, tensor_id, step), sigma_scale);
@@ -143,6 +147,7 @@ int ark_synth_normal_f32(float* out, uint64_t n, uint64_t seed,
                          void* stream) {
   if (n == 0) return 0;
   if (!out) return -1;
+  written(out, n * 4u);
   hipLaunchKernelGGL(normal_kernel<false>, dim3(grid_for(n)), dim3(256), 0,
                      (hipStream_t)stream, (void*)out, n,
                      synth_base(seed, tensor_id, step), sigma_scale);
@@ -155,6 +160,7 @@ int ark_synth_copy(void* dst, const void* src, uint64_t nbytes, void* stream) {
   const uint64_t n = nbytes / 16u;
   const uint64_t blocks = (n + 255) / 256;
   if (blocks > 0xFFFFFFFFull / 256u) return -1;
+  written(dst, nbytes);
   hipLaunchKernelGGL(copy_kernel, dim3((uint32_t)blocks), dim3(256), 0,
                      (hipStream_t)stream, (u32x4*)dst, (const u32x4*)src, n);
   return status(hipGetLastError());
@@ -168,6 +174,9 @@ int ark_synth_stream_mix(uint16_t* w, const uint16_t* g, float* m, float* v, uin
     return -1;
   const uint64_t rows = n / 256u;
   if (rows > 0x7FFFFFFFull / 64u) return -1;
+  written(w, n * 2u);
+  written(m, n * 4u);
+  written(v, n * 4u);
   const uint32_t lds =
       ark::resident_lds_bytes((const void*)stream_mix_kernel, 64, (int)blocks_per_cu);
   hipLaunchKernelGGL(stream_mix_kernel, dim3((uint32_t)rows), dim3(64), lds, (hipStream_t)stream,
@@ -178,6 +187,7 @@ int ark_synth_stream_mix(uint16_t* w, const uint16_t* g, float* m, float* v, uin
 int ark_synth_fill_u16(uint16_t* out, uint64_t n, uint16_t bits, void* stream) {
   if (n == 0) return 0;
   if (!out) return -1;
+  written(out, n * 2u);
   hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0,
                      (hipStream_t)stream, out, n, bits);
   return status(hipGetLastError());

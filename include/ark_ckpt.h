@@ -83,10 +83,16 @@ typedef struct ark_ckpt_info {
  * "<target>.tmp.<pid>.<n>" (created exclusively, unique to the call) and
  * renames it over the target once complete, so a failed save leaves no
  * partial file and an existing file unchanged.  The target is path, or the
- * file a symbolic link at path resolves to (the link is kept, as File::create
- * keeps it; io.rs:450).  amp may be NULL (no trailer).  The records are read
- * on the given stream; the call returns when the file is written, flushed,
- * closed and renamed. */
+ * file a symbolic link at path names, followed link by link as open(2) does,
+ * also when the link dangles (the link is kept and the file it names is
+ * created, as File::create does; io.rs:450).  A new file gets mode 0666 less
+ * the umask (File::create's); a file replaced hands its mode, and where
+ * permitted its owner and group, on to the new file, as File::create keeps
+ * them by truncating in place.  One difference remains: other hard links to
+ * a replaced file keep naming the old contents, where File::create would
+ * have rewritten the one file they share.  amp may be NULL (no trailer).
+ * The records are read on the given stream; the call returns when the file
+ * is written, flushed, closed and renamed. */
 int ark_ckpt_save_v4(const char *path, uint64_t global_step, uint64_t adam_step,
                      const ark_ckpt_record *records, int32_t n_records,
                      const ark_opt_state *amp, void *stream);

@@ -74,11 +74,12 @@ int ark_grad_embed_scatter(float *embed_grad, uint32_t vocab, uint32_t d,
  *   ark_grad_embed_scatter_final(..., opt);          the token scatter
  *   ark_opt_step(opt, lr, info);
  * Between the final calls and the step, a write to the handle's gradients
- * through this library's other calls (ark_grad_accumulate,
- * ark_grad_plan_run, ark_grad_embed_scatter, ark_grad_embed_scatter_noalloc)
- * discards the units; a write the library does not see (the caller's own
- * kernel or copy) must not happen: the step would use the units of the old
- * values.  ark_opt_set_state and ark_opt_record_overflow discard the units
+ * through any other call of this library (ark_grad_accumulate,
+ * ark_grad_plan_run, ark_grad_embed_scatter, ark_grad_embed_scatter_noalloc,
+ * the codec's dequantisation and plans, a checkpoint load or unpack, the
+ * single-tensor Adam steps, the synthetic-input writers) discards the units;
+ * a write the library does not see (the caller's own kernel or copy) must
+ * not happen: the step would use the units of the old values.  ark_opt_set_state and ark_opt_record_overflow discard the units
  * (the loss scale changes), as does every ark_opt_step after using them; a
  * step without fresh units reads the gradients as usual. */
 
@@ -101,26 +102,39 @@ int ark_grad_embed_scatter_final(float *embed_grad, uint32_t vocab, uint32_t d,
                                  const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                                  ark_opt_handle *opt);
 
-/* Size of the device array behind ark_grad_embed_scatter_noalloc: 48 MiB
- * per GPU, held from the first call on that GPU until the process ends. */
+/* Size of the device array behind ark_grad_embed_scatter_noalloc: 48 MiB.
+ * The array is part of the library's code object, so every GPU the library is
+ * used on holds one, from the library's first kernel launch or device set-up
+ * there until the process ends, whether or not it calls this scatter. */
 #define ARK_GRAD_SCRATCH_BYTES (48ull << 20)
 
 /* ark_grad_embed_scatter with the same arguments and bit-identical results,
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No
- * counterpart in the reference.  Its workspace is a static device array of
+ * counterpart in the reference.  Its workspace is the static device array of
  * ARK_GRAD_SCRATCH_BYTES per GPU instead of the stream-ordered pool, so it
- * calls no hipMalloc, hipFree or other allocating routine (the first call on
- * a GPU looks the array's address up once).  The workspace is
+ * calls no hipMalloc, hipFree or other allocating routine.  The workspace is
  *   8 * batch_seq bytes, plus 8 * batch_seq + 1024 * ceil(batch_seq / 4096)
  *   more when batch_seq > 4096, plus 4 * batch_seq * d,
  * each part rounded up to 256 bytes (a 2 x 2048-token batch at d = 768
  * needs 12.6 MB, at d = 2048 33.6 MB); a larger one is rejected with
- * ARK_OPT_EINVAL before anything is queued.  Every call on a GPU shares that
- * GPU's array, and each call writes every workspace byte it reads, so
- * nothing carries over from the previous call; calls that overlap on one
- * GPU (two streams, or two host threads) race on the array and must be
- * serialised by the caller. */
+ * ARK_OPT_EINVAL before anything is queued.
+ *
+ * Set-up: once per GPU the library looks the array's address up and creates
+ * one event; ark_opt_create and ark_grad_plan_create do this for their GPU,
+ * and so does this call's first use on a GPU not yet set up.  That first use
+ * must not come under graph capture: it then returns ARK_OPT_EINVAL before
+ * anything is queued.
+ *
+ * Every call on a GPU shares that GPU's array, and each call writes every
+ * workspace byte it reads, so nothing carries over from the previous call.
+ * The library orders the calls on one GPU: a call outside graph capture, on
+ * any stream and from any host thread, makes its stream wait
+ * (hipStreamWaitEvent) for the work of the previous such call before it
+ * touches the array.  A call made under graph capture becomes graph nodes
+ * that this ordering does not cover: the caller orders each replay of that
+ * graph against other uses of the array on the GPU (for instance by
+ * replaying on the stream that makes the eager calls). */
 int ark_grad_embed_scatter_noalloc(float *embed_grad, uint32_t vocab, uint32_t d,
                                    const uint32_t *tokens, const float *dx0, uint32_t batch_seq,
                                    void *stream);

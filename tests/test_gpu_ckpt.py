@@ -660,6 +660,57 @@ def test_failed_save_keeps_the_earlier_state(tmp_path):
     assert sorted(os.listdir(tmp_path)) == ["ckpt.ark", "latest.ark", "real.ark", "ro"]
 
 
+def test_save_keeps_modes_and_follows_links_as_file_create(tmp_path):
+    """File::create (io.rs:450) semantics the save keeps although it writes a
+    temporary file and renames it: a new file gets mode 0666 less the umask;
+    a replaced file's mode carries over; a chain of symbolic links with
+    relative targets is followed to the file it names, which becomes the
+    checkpoint while the links stay; a dangling link is followed too, and
+    the file it names is created."""
+    import os
+    import stat
+    import torch
+    from ark_amd._lib import lib
+    L = lib()
+    w = torch.arange(300, dtype=torch.float32, device="cuda").half()
+    recs = (_abi.CkptRecord * 1)()
+    recs[0] = _abi.CkptRecord(w.data_ptr(), 300, _abi.CKPT_F16, 0)
+    want = K.write_v4(5, 6, [w.cpu().numpy().view(np.uint16)])
+
+    def save(p):
+        rc = L.ark_ckpt_save_v4(os.fsencode(str(p)), 5, 6, recs, 1, None, None)
+        assert rc == 0, L.ark_opt_last_error().decode()
+
+    umask = os.umask(0o022)
+    os.umask(umask)
+    new = tmp_path / "new.ark"
+    save(new)
+    assert stat.S_IMODE(new.stat().st_mode) == 0o666 & ~umask and new.read_bytes() == want
+    for mode in (0o600, 0o640, 0o604):
+        old = tmp_path / f"old{mode:o}.ark"
+        old.write_bytes(b"earlier")
+        old.chmod(mode)
+        save(old)
+        assert stat.S_IMODE(old.stat().st_mode) == mode and old.read_bytes() == want
+    # link -> link2 -> d/real.ark, targets relative to each link's directory
+    (tmp_path / "d").mkdir()
+    real = tmp_path / "d" / "real.ark"
+    real.write_bytes(b"old")
+    real.chmod(0o640)
+    (tmp_path / "link2").symlink_to("d/real.ark")
+    (tmp_path / "link").symlink_to("link2")
+    save(tmp_path / "link")
+    assert os.readlink(tmp_path / "link") == "link2"
+    assert os.readlink(tmp_path / "link2") == "d/real.ark"
+    assert real.read_bytes() == want and stat.S_IMODE(real.stat().st_mode) == 0o640
+    # a dangling link: the link stays and the file it names is created
+    (tmp_path / "dangling").symlink_to("d/created.ark")
+    save(tmp_path / "dangling")
+    assert (tmp_path / "dangling").is_symlink()
+    assert (tmp_path / "d" / "created.ark").read_bytes() == want
+    assert sorted(os.listdir(tmp_path / "d")) == ["created.ark", "real.ark"]
+
+
 @pytest.mark.parametrize("kind", ["v4_without_gamma_final", "v2_weights_only"])
 def test_load_params_follows_the_file(tmp_path, kind):
     """load_params on the files the reference also resumes from: a V4 file

@@ -2,11 +2,13 @@
 (ark_grad_plan_run_final, ark_grad_embed_scatter_final; include/ark_grad.h)
 against the same step reading the gradients (ark_opt_step's own norm pass):
 the global sum of squares must keep its bits, so every step scalar and every
-w/m/v element of the two paths must be identical.  The oracle's agreement
-with the reading path is what tests/test_gpu_parity.py and
-tests/test_gpu_grad.py establish; here the two device paths are compared on
-the full EKO-237M set, on ragged and unaligned tables, with non-finite
-values entering through either producer, and on misuse."""
+w/m/v element of the two paths must be identical.  On the full EKO-237M
+set both paths are also compared with the oracle's gradient loops and
+optimizer (test_eko237m_fp32_gradients_both_paths_against_the_oracle); the
+rest compares the two device paths with each other on ragged and unaligned
+tables, with non-finite values entering through either producer, and on
+misuse, the reading path's own agreement with the oracle being what
+tests/test_gpu_parity.py and tests/test_gpu_grad.py establish."""
 import numpy as np
 import pytest
 
@@ -118,6 +120,90 @@ def test_eko237m_units_step_matches_the_reading_step():
         r.close()
 
 
+def test_eko237m_fp32_gradients_both_paths_against_the_oracle():
+    """The reference's own gradient type (fp32, memory.rs:239-243) at full
+    size: all 272 EKO-237M tensors, gradients zeroed (training.rs:248), then
+    two accumulations of seeded backward outputs (bridge.m:910-915,
+    :931-947) -- the second through ark_grad_plan_run_final on the units
+    path -- and a 4096-token Zipf scatter at d 768 (bridge.m:922-928) --
+    ark_grad_embed_scatter_final on the units path -- then one step.  Two
+    fresh-gradient steps, the first clipped and the second not
+    (optimizer.rs:145-149).  Each path's gradients, step scalars and every
+    w/m/v element are compared bit for bit with the oracle's loops and
+    optimizer on the host (training.rs:289-314), not only with each
+    other."""
+    torch = _torch()
+    import oracle
+    from ark_amd import synth
+    from oracle import harness as H
+    specs = EKO_237M.tensors()
+    e = [s.name for s in specs].index("embed")
+    vocab, d, n_tok = 32000, 768, 4096
+    seed, scale, lr = 23, 65536.0, HP["lr"]
+    base = synth.log_uniform_sigmas(len(specs), seed)
+    est = float(np.sqrt(sum(s.n * float(x) ** 2 for s, x in zip(specs, base))))
+    # step 0 as drawn (norm ~ 50: clips); step 1 scaled to a norm of ~0.6
+    sigs = [base, [float(x) * 0.4 / est for x in base]]
+    ps = [synth.problem(specs, seed, HP["weight_decay"], base, scale,
+                        grad_dtype=_abi.GRAD_F32) for _ in range(2)]
+    from ark_amd.optimizer import AdamConfig, AmpConfig, Optimizer
+    cfg = AdamConfig(**HP)
+    opts = [Optimizer(cfg, p, AmpConfig(loss_scale_init=scale, loss_scale_max=2.0 ** 24))
+            for p in ps]
+    outs = [torch.empty(s.n, dtype=torch.float32, device="cuda") for s in specs]
+    plans = [grad.GradPlan([(p.g(i), outs[i]) for i in range(len(specs))]) for p in ps]
+    ts = H.host_problem(specs, seed, HP["weight_decay"], base, scale,
+                        grad_dtype=_abi.GRAD_F32, nthreads=8)
+    ref = oracle.Optimizer(ts, opts[0].hp, nthreads=8)
+    rng = np.random.default_rng(seed)
+    for k in range(2):
+        tokens = ((rng.zipf(1.2, n_tok) - 1) % vocab).astype(np.uint32)
+        dx0 = (rng.standard_normal((n_tok, d)) * (sigs[k][e] * scale)).astype(np.float32)
+        tok_d = torch.from_numpy(tokens.view(np.int32)).cuda()
+        dx0_d = torch.from_numpy(dx0).cuda()
+        for p in ps:
+            for i in range(len(specs)):
+                p.g(i).zero_()
+        host_out = []
+        for a in range(2):  # two accumulations, the backward outputs regenerated between
+            st = 100 + 2 * k + a
+            for i, s in enumerate(specs):
+                ss = synth.grad_sigma_scale(sigs[k][i], scale)
+                synth.normal_f32(outs[i], seed, i, st, ss)
+            host_out.append(st)
+            for p, plan, opt, fused in zip(ps, plans, opts, (False, True)):
+                plan.run(final_for=opt if (fused and a == 1) else None)
+        for p, opt, fused in zip(ps, opts, (False, True)):
+            grad.embed_scatter(p.g(e).view(vocab, d), tok_d, dx0_d,
+                               final_for=opt if fused else None)
+        infos = [opt.step_all(lr, info=True)[1] for opt in opts]
+
+        def host_grads(i):
+            t = ts[i]
+            t.g[:] = 0.0
+            for st in host_out:
+                oracle.grad_accumulate(t.g, oracle.synth_normal_f32(
+                    t.n, seed, i, st, synth.grad_sigma_scale(sigs[k][i], scale)))
+        H._pmap(host_grads, range(len(specs)), 8)
+        oracle.embed_scatter(ts[e].g.reshape(vocab, d), tokens, dx0)
+        _, ri = ref.step(lr)
+        assert ri.applied == 1 and ri.clipped == (1 if k == 0 else 0), (k, ri.grad_norm)
+        for name, p, gi in zip(("reading", "units"), ps, infos):
+            diff = H.info_matches(gi, ri)
+            assert not diff, (k, name, diff)
+            c = H.compare(p, ts, nthreads=8)
+            assert c["w"] == c["m"] == c["v"] == 0, (k, name, c)
+        # the reading path's gradients are the oracle's loops' bit for bit
+        # (the units path's are the same buffers' values; its step did not read them)
+        for i in (e, 1, len(specs) - 1):
+            assert np.array_equal(H.to_host(ps[0].g(i)).view(np.uint32),
+                                  ts[i].g.view(np.uint32)), (k, specs[i].name)
+    for plan in plans:
+        plan.close()
+    for opt in opts:
+        opt.close()
+
+
 def test_ragged_unaligned_tables_and_small_norm_blocks():
     """Tensors of 1, 255, 256, 257, 4095, 4097 and 9000 elements (units
     partly and wholly past a segment's end), a backward output that is only
@@ -211,13 +297,18 @@ def test_units_are_discarded_when_the_loss_scale_or_gradients_change():
     a.close(), b.close()
 
 
-@pytest.mark.parametrize("route", ["accumulate", "plan", "scatter", "scatter_noalloc"])
+@pytest.mark.parametrize("route", ["accumulate", "plan", "scatter", "scatter_noalloc", "dequant",
+                                   "codec_plan", "ckpt_unpack", "adam_dropin"])
 def test_library_gradient_writes_after_the_final_calls_drop_the_units(route):
     """After the final accumulation, a further write to a gradient through
-    the library's plain calls (ark_grad_accumulate, ark_grad_plan_run,
-    ark_grad_embed_scatter and its no-allocation form) makes the next step
-    read the gradients instead of the units the final call wrote: the step
-    equals, bit for bit, that of a twin problem that never had units."""
+    the library's other calls (ark_grad_accumulate, ark_grad_plan_run,
+    ark_grad_embed_scatter and its no-allocation form, the codec's
+    dequantisation and plan, a checkpoint unpack, a single-tensor Adam step
+    whose m is that buffer) makes the next step read the gradients instead
+    of the units the final call wrote: the step equals, bit for bit, that of
+    a twin problem that never had units."""
+    from ark_amd import ckpt, codec
+    from ark_amd._lib import lib as lib_
     torch = _torch()
     specs = EkoConfig(n_layers=1, d_model=256, hidden=512, vocab=100).tensors()
     e = [s.name for s in specs].index("embed")
@@ -237,6 +328,27 @@ def test_library_gradient_writes_after_the_final_calls_drop_the_units(route):
             grad.accumulate(r.ps.g(1), extra[1])
         elif route == "plan":
             r.plan.run()
+        elif route == "dequant":
+            codec.dequant_f16_to_f32(extra[1].half(), r.ps.g(1))
+        elif route == "codec_plan":
+            src = extra[1].half()
+            cp = codec.CodecPlan([(src, r.ps.g(1))], "f16_to_f32")
+            cp.run()
+            torch.cuda.synchronize()
+            cp.close()
+        elif route == "ckpt_unpack":
+            image = torch.empty(ckpt.image_bytes([extra[1]]), dtype=torch.uint8, device="cuda")
+            ckpt.pack([extra[1]], image, 1, 1)
+            ckpt.unpack(image, [r.ps.g(1)])
+        elif route == "adam_dropin":
+            # the gradient buffer used as another tensor's first moment
+            n = r.ps.g(1).numel()
+            w = torch.zeros(n, dtype=torch.float16, device="cuda")
+            v = torch.zeros(n, device="cuda")
+            assert lib_().ark_hip_adam_step_f16(w.data_ptr(), extra[1].data_ptr(),
+                                                r.ps.g(1).data_ptr(), v.data_ptr(), n,
+                                                3e-4, 0.9, 0.95, 1e-8, 0.0, 1,
+                                                torch.cuda.current_stream().cuda_stream) == 0
         else:
             grad.embed_scatter(r.ps.g(e).view(100, 256), tokens, dx0,
                                noalloc=(route == "scatter_noalloc"))
