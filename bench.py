@@ -73,17 +73,19 @@ def sigmas_for(name, specs):
     return [w["sigma"]] * len(specs)
 
 
-def run_gpu(name, steps, warmup, grad="f16"):
+def run_gpu(name, steps, warmup, grad="f16", skip=False):
+    """skip: also time skipped steps on the same handle afterwards (always
+    for c3; c2's tensor set is c3's)."""
     import torch
     torch.cuda.set_device(0)
     # everything on one non-default stream, so the step can also be captured
     # in a HIP graph
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        return _run_gpu(name, steps, warmup, stream, grad)
+        return _run_gpu(name, steps, warmup, stream, grad, skip)
 
 
-def _run_gpu(name, steps, warmup, stream, grad="f16"):
+def _run_gpu(name, steps, warmup, stream, grad="f16", skip=False):
     import torch
     from ark_amd import _abi, synth
     from ark_amd.eko import config_tensors
@@ -93,9 +95,10 @@ def _run_gpu(name, steps, warmup, stream, grad="f16"):
     w = WORKLOADS[name]
     sig = sigmas_for(name, specs)
     cfg = AdamConfig(**HP)
-    # c3 times skipped steps back to back: no early stop after 200 of them
+    skip = skip or name == "c3"
+    # skipped steps are timed back to back: no early stop after 200 of them
     amp = AmpConfig(loss_scale_init=w["loss_scale"], loss_scale_max=2.0 ** 24,
-                    max_consecutive_nonfinite=(2 ** 31 if name == "c3" else 200))
+                    max_consecutive_nonfinite=(2 ** 31 if skip else 200))
     log(f"[bench] building {name}: {sum(s.n for s in specs)} params, {len(specs)} tensors")
     gdt = _abi.GRAD_F16 if grad == "f16" else _abi.GRAD_F32
     ps = synth.problem(specs, SEED, cfg.weight_decay, sig, w["loss_scale"], grad_dtype=gdt)
@@ -141,7 +144,7 @@ def _run_gpu(name, steps, warmup, stream, grad="f16"):
     del graph
 
     _, last = opt.step_all(cfg.lr, info=True)
-    skip = _time_skipped(ps, opt, cfg, steps) if name == "c3" else None
+    skip = _time_skipped(ps, opt, cfg, steps) if skip else None
     n = ps.n_params
     res = dict(skip=skip,
         n_params=n, n_tensors=len(specs), ms_step=ms_step,
@@ -184,11 +187,13 @@ def _time_skipped(ps, opt, cfg, steps):
     g16[0] = old
     assert last.applied == 0 and last.state.skipped_steps >= 2 * steps + 2
     log(f"[bench] skipped step: {wall_ms:.4f} ms (norm {tm.ms_norm / tm.steps:.4f}, finalize "
-        f"{tm.ms_finalize / tm.steps:.4f}, adamw exit {tm.ms_adamw / tm.steps:.4f})")
+        f"{tm.ms_finalize / tm.steps:.4f})")
+    # the AdamW launch's own event interval is left out: events around a
+    # launch whose blocks all exit at once read longer than the whole
+    # skipped step's wall clock; rocprofv3's kernel trace times that dispatch
     return dict(ms_per_skipped_step=round(wall_ms, 4),
                 kernels_ms={"sumsq": round(tm.ms_norm / tm.steps, 4),
-                            "finalize": round(tm.ms_finalize / tm.steps, 4),
-                            "adamw_exit": round(tm.ms_adamw / tm.steps, 4)},
+                            "finalize": round(tm.ms_finalize / tm.steps, 4)},
                 skipped_total=int(last.state.skipped_steps))
 
 
@@ -414,19 +419,57 @@ def run_cpu_baseline(name, budget_s, threads, grad="f16"):
                        f"{'8-wide AVX2/F16C' if vec else 'scalar'} loops")
 
 
-def traffic_from_profiles(name, kernel="adamw_kernel"):
-    """HBM-side bytes per launch of `kernel` measured by rocprofv3 byte
-    counters (calibrated against a plain copy) for this workload, from the
-    committed profile summary; None when no profile of it is committed."""
+def profile_summary(name, kernel="adamw_kernel"):
+    """The committed rocprofv3 figures of `kernel` on this workload
+    (profiles/<kernel>_<name>_traffic.txt): HBM-side bytes per launch from
+    the byte counters, calibrated against a plain copy, and the kernel
+    trace's average launch duration; {} when none is committed."""
     p = os.path.join(ROOT, "profiles", f"{kernel}_{name}_traffic.txt")
     if not os.path.exists(p):
-        return None, None
+        return {}
     kv = {}
     for line in open(p):
         if ":" in line and not line.startswith("#"):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.strip()
+    return kv
+
+
+def traffic_from_profiles(name, kernel="adamw_kernel"):
+    """(bytes per launch, source) from profile_summary; (None, None) when no
+    profile of it is committed."""
+    kv = profile_summary(name, kernel)
+    if not kv:
+        return None, None
     return int(kv["bytes_per_launch"]), kv.get("source")
+
+
+def secondary_c4(steps, warmup):
+    """The 1.3B scale-up (c4) step timed the same way as the headline, on a
+    problem built after the headline's was freed; no CPU leg."""
+    r = run_gpu("c4", steps, warmup, "f16")
+    n = r["n_params"]
+    b_step, b_adamw = step_bytes("f16")
+    gbs = b_step * n / (r["ms_step"] * 1e-3) / 1e9
+    adam_gbs = b_adamw * n / (r["ms_adamw"] * 1e-3) / 1e9
+    out = dict(workload=f"c4: {WORKLOADS['c4']['desc']}", params=n, tensors=r["n_tensors"],
+               ms_per_step=round(r["ms_step"], 4), gbs=round(gbs, 2),
+               frac_of_peak_hbm=round(gbs / PEAK_HBM_GBS, 4),
+               bytes_per_step=b_step * n, clipped=r["clipped"],
+               hip_graph_ms_per_step=round(r["graph_ms"], 4),
+               kernels_ms={"sumsq": round(r["ms_norm"], 4), "finalize": round(r["ms_finalize"], 4),
+                           "adamw": round(r["ms_adamw"], 4)},
+               adamw=dict(achieved=round(adam_gbs, 2), unit="GB/s",
+                          frac=round(adam_gbs / PEAK_HBM_GBS, 4),
+                          algorithmic_bytes_per_launch=b_adamw * n))
+    kv = profile_summary("c4")
+    if kv:
+        ns = float(kv["avg_launch_ns"])
+        out["adamw"].update(
+            traffic=int(kv["bytes_per_launch"]), profile_avg_us=round(ns / 1e3, 1),
+            profile_frac=round(b_adamw * n / (ns * 1e-9) / 1e9 / PEAK_HBM_GBS, 4),
+            profile_source=kv.get("source"))
+    return out
 
 
 def run_codec(a):
@@ -823,6 +866,9 @@ def main():
                          "fp32 weights (ark_hip_adam_step)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="c2 headline only: without the skipped-step (c3) and 1.3B (c4) figures "
+                         "the default line also carries")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the optimizer step of this build runs on a "
@@ -835,7 +881,12 @@ def main():
             calib_copy()
         return
 
-    r = run_gpu(a.workload, a.steps, a.warmup, a.grad)
+    # the default line (c2, fp16 gradients) also carries the secondary
+    # configurations: a skipped step (c3's set is c2's, so the c2 handle
+    # times it) and the 1.3B scale-up (c4)
+    secondary = a.workload == "c2" and a.grad == "f16" and not a.no_secondary
+    r = run_gpu(a.workload, a.steps, a.warmup, a.grad, skip=secondary)
+    c4 = secondary_c4(a.steps, a.warmup) if secondary else None
     if a.calib_copy:
         calib_copy()
     n = r["n_params"]
@@ -891,7 +942,18 @@ def main():
         },
         "cpu_baseline": cpu,
     }
-    if r.get("skip"):
+    if secondary:
+        out["secondary"] = {
+            "c3_skipped_step": dict(
+                r["skip"], workload="c3: the c2 set with +inf in one fp16 gradient",
+                bytes_per_skipped_step=2 * n,
+                note="the norm pass reads g (2 B/param) and flags it, the finalize skips and "
+                     "halves the loss scale, the AdamW pass exits before any access; the rest "
+                     "of the wall clock is that exiting launch's dispatch (kernel trace: "
+                     "profiles/adamw_kernel_c3.md)"),
+            "c4": c4,
+        }
+    elif r.get("skip"):
         out["config"]["skipped_steps"] = dict(
             r["skip"], ms_per_applied_step=round(r["ms_step"], 4),
             bytes_per_skipped_step=2 * n,
