@@ -46,6 +46,7 @@ def _declare(L):
         "ark_opt_get_timing": ([H, C.POINTER(_abi.Timing)], C.c_int),
         "ark_hip_adam_step_f16": ([P, P, P, P, u64, f32, f32, f32, f32, f32, u32, P], C.c_int),
         "ark_hip_adam_step": ([P, P, P, P, u64, f32, f32, f32, f32, f32, u32, P], C.c_int),
+        "ark_hip_grad_clip": ([P, u64, f32, C.POINTER(f32), P], C.c_int),
         "ark_synth_normal_f16": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_normal_f32": ([P, u64, u64, u32, u32, f32, P], C.c_int),
         "ark_synth_fill_u16": ([P, u64, C.c_uint16, P], C.c_int),

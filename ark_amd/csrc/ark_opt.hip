@@ -605,6 +605,45 @@ int ark_hip_adam_step_f16(uint16_t* w, const float* g, float* m, float* v,
   return ARK_OPT_OK;
 }
 
+int ark_hip_grad_clip(float* grads, uint64_t n, float threshold, float* norm_out,
+                      void* stream) {
+  if (norm_out) *norm_out = 0.0f;
+  if (n == 0) return ARK_OPT_OK;  // no value: norm 0, nothing scaled (ffi.rs:208-210)
+  if ((uintptr_t)grads & 3u) return fail(ARK_OPT_EINVAL, "grads not 4-byte aligned");
+  if (n > ark::kClipMaxElements)
+    return fail(ARK_OPT_EINVAL, "n = %llu exceeds %llu", (unsigned long long)n,
+                (unsigned long long)ark::kClipMaxElements);
+  int rc;
+  if ((rc = check_buffer(grads, n * 4u, "grads", 0))) return rc;
+  {
+    const void* d = grads;  // it may be an optimizer's gradient
+    const uint64_t b = n * 4u;
+    ark::opt_units_invalidate(&d, &b, 1);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const uint32_t nparts = ark::clip_parts(n);
+  const uint32_t ngroups = (nparts + ark::kFoldGroup - 1) / ark::kFoldGroup;
+  const size_t bytes = ark::align_up(sizeof(ark::ClipScalars), 256) +
+                       ark::align_up((size_t)nparts * 8u, 256) + (size_t)ngroups * 8u;
+  ark::StreamBuf ws;
+  hipError_t e = ws.alloc(bytes, s);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ARK_OPT_ENOMEM, "hipMallocAsync(%zu) for the clip failed", bytes);
+  }
+  ark::ClipScalars* cs = (ark::ClipScalars*)ws.p;
+  double* parts = (double*)((char*)ws.p + ark::align_up(sizeof(ark::ClipScalars), 256));
+  double* folded = parts + ark::align_up((size_t)nparts * 8u, 256) / 8u;
+  ARK_HIP(ark::launch_grad_clip(grads, n, threshold, parts, folded, cs, s));
+  if (norm_out) {
+    float norm = 0.0f;
+    ARK_HIP(hipMemcpyAsync(&norm, &cs->norm, sizeof(float), hipMemcpyDeviceToHost, s));
+    ARK_HIP(hipStreamSynchronize(s));
+    *norm_out = norm;
+  }
+  return ARK_OPT_OK;
+}
+
 }  // extern "C"
 
 // ---- the norm's units, for the gradient hand-off (ark_opt_internal.hpp) ----

@@ -704,7 +704,184 @@ __global__ __launch_bounds__(64) void adamw_single_w32_kernel(
   }
 }
 
+// ---- the single-tensor clip (ark_asm_grad_clip, opti.s:369-432) ----------
+
+// Block b covers elements [b * 2 * kSeg, (b + 1) * 2 * kSeg) of one fp32
+// array and writes the pairwise tree of its squares: the same lane layout and
+// reduction as sumsq_kernel<float, 2> over a one-tensor table, so the partial
+// is an aligned subtree of the canonical tree.  No non-finite flag: an inf
+// value squares to inf and a NaN to NaN, and the f64 tree carries them (+inf
+// unless a NaN is present), as the reference's fmla chain does.
+// Blocks run last to first, and blocks from nt_from up read with
+// non-temporal loads, so the first kNormCachedBytes of the array, read last,
+// stay in the Infinity Cache for clip_scale_kernel, which starts there.
+__global__ __launch_bounds__(kBlock) void clip_norm_kernel(const float* __restrict__ g,
+                                                           uint64_t n, uint32_t vec,
+                                                           uint32_t nt_from,
+                                                           double* __restrict__ part_sum) {
+  constexpr int V = 4;  // two segments, two halves each
+  __shared__ double lds[kBlock / 64][V];
+  const uint32_t blk = gridDim.x - 1u - blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint64_t base = (uint64_t)blk * (2u * kSeg);
+  const float* p = g + base;
+  double vals[V];
+  uint32_t bad = 0;  // unused: non-finite values stay in the sum
+  if (vec && base + 2u * kSeg <= n) {
+    GradIO<float>::Raw8 raw[V];
+    if (blk >= nt_from) {
+#pragma unroll
+      for (int h = 0; h < V; ++h)
+        raw[h] = GradIO<float>::load8<true>(p + h * kHalfSeg + tid * kVec);
+    } else {
+#pragma unroll
+      for (int h = 0; h < V; ++h)
+        raw[h] = GradIO<float>::load8<false>(p + h * kHalfSeg + tid * kVec);
+    }
+#pragma unroll
+    for (int h = 0; h < V; ++h) {
+      float f[kVec];
+      GradIO<float>::unpack8(raw[h], f, bad);
+      vals[h] = group_sum(f, 1.0f);
+    }
+  } else {
+    const uint64_t left = n - base;
+#pragma unroll
+    for (int h = 0; h < V; ++h) {
+      const uint64_t e0 = (uint64_t)h * kHalfSeg + (uint64_t)tid * kVec;
+      float f[kVec];
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) f[j] = (e0 + j < left) ? ld_g<float>(p + e0 + j) : 0.0f;
+      vals[h] = group_sum(f, 1.0f);
+    }
+  }
+  int idx = 0;
+  transpose_reduce<V, 0>(vals, lane, idx);
+  const double wsum = butterfly_from<log2i(V)>(vals[0]);
+  if (lane < V) lds[wave][idx] = wsum;
+  __syncthreads();
+  if (wave == 0) {
+    double x = 0.0;
+    if (lane < V) x = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+#pragma unroll
+    for (int st = 0; st < log2i(V); ++st) x = x + __shfl_xor(x, 1 << st);
+    if (tid == 0) part_sum[blk] = x;
+  }
+}
+
+// fold_kernel over nparts partials read as zero past the last one.
+__global__ __launch_bounds__(kFoldGroup) void clip_fold_kernel(const double* __restrict__ in,
+                                                               uint32_t nparts,
+                                                               double* __restrict__ out) {
+  const uint32_t i = blockIdx.x * kFoldGroup + threadIdx.x;
+  double x = i < nparts ? in[i] : 0.0;
+  x = butterfly_from<0>(x);
+  if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
+
+// The root of the tree over nparts leaves (zero past them, padded to
+// kFinThreads * L), as finalize_kernel forms it; then the decision of
+// opti.s:399-404: norm = fsqrt of the sum as fp32 (the reference's sum is
+// fp32), clipped when norm > threshold (fcmp + b.le: an unordered compare
+// does not clip), coefficient threshold / norm.
+template <int L>
+__global__ __launch_bounds__(kFinThreads) void clip_finalize_kernel(
+    const double* __restrict__ leaves, uint32_t nparts, float threshold,
+    ClipScalars* __restrict__ out) {
+  __shared__ double wsum[kFinThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  double q[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const uint32_t i = (uint32_t)tid * L + j;
+    q[j] = i < nparts ? leaves[i] : 0.0;
+  }
+#pragma unroll
+  for (int w = L / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int j = 0; j < w; ++j) q[j] = q[2 * j] + q[2 * j + 1];
+  double x = butterfly_from<0>(q[0]);
+  if (lane == 0) wsum[wave] = x;
+  __syncthreads();
+  if (wave != 0) return;
+  double y = lane < kFinThreads / 64 ? wsum[lane] : 0.0;
+#pragma unroll
+  for (int s = 0; s < log2i(kFinThreads / 64); ++s) y = y + __shfl_xor(y, 1 << s);
+  if (lane != 0) return;
+  ClipScalars c;
+  c.sumsq = y;
+  c.norm = sqrtf((float)y);
+  c.clipped = c.norm > threshold ? 1u : 0u;
+  c.coef = c.clipped ? threshold / c.norm : 1.0f;
+  *out = c;
+}
+
+// g[i] = g[i] * coef (fmul, opti.s:409-420) when the finalize decided to
+// clip; otherwise every block exits at once.  Grid-stride over 4-element
+// groups.
+__global__ __launch_bounds__(256) void clip_scale_kernel(float* __restrict__ g, uint64_t n,
+                                                         uint32_t vec,
+                                                         const ClipScalars* __restrict__ cs) {
+  const uint32_t clipped = cs->clipped;
+  const float coef = cs->coef;
+  if (!clipped) return;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u * 4u;
+  for (uint64_t e = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u; e < n; e += stride) {
+    if (vec && e + 4u <= n) {
+      f32x4 x = ld_nt<f32x4>(g + e);
+      x.x = x.x * coef;
+      x.y = x.y * coef;
+      x.z = x.z * coef;
+      x.w = x.w * coef;
+      st_nt<f32x4>(g + e, x);
+    } else {
+      for (uint64_t j = e; j < e + 4u && j < n; ++j) st_g<float>(g + j, ld_g<float>(g + j) * coef);
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_grad_clip(float* g, uint64_t n, float threshold, double* parts,
+                            double* folded, ClipScalars* out, hipStream_t stream) {
+  const uint32_t nparts = clip_parts(n);
+  const uint32_t vec = ((uintptr_t)g & 15u) == 0 ? 1u : 0u;
+  const uint32_t nt_from = (uint32_t)(kNormCachedBytes / (2u * kSeg * sizeof(float)));
+  hipLaunchKernelGGL(clip_norm_kernel, dim3(nparts), dim3(kBlock), 0, stream, g, n, vec, nt_from,
+                     parts);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const double* leaves = parts;
+  uint32_t nleaves = nparts;
+  if (nparts > kFinTarget) {
+    const uint32_t groups = (nparts + kFoldGroup - 1) / kFoldGroup;
+    hipLaunchKernelGGL(clip_fold_kernel, dim3(groups), dim3(kFoldGroup), 0, stream, parts,
+                       nparts, folded);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    leaves = folded;
+    nleaves = groups;
+  }
+  const dim3 one(1), fin(kFinThreads);
+#define ARK_CLIP_FIN(L)                                                                         hipLaunchKernelGGL((clip_finalize_kernel<L>), one, fin, 0, stream, leaves, nleaves, threshold,                      out)
+  switch (finalize_leaves(nleaves)) {
+    case 1: ARK_CLIP_FIN(1); break;
+    case 2: ARK_CLIP_FIN(2); break;
+    case 4: ARK_CLIP_FIN(4); break;
+    case 8: ARK_CLIP_FIN(8); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef ARK_CLIP_FIN
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  uint64_t blocks = (n + 1023u) / 1024u;
+  if (blocks > 65536u) blocks = 65536u;
+  hipLaunchKernelGGL(clip_scale_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, g, n, vec,
+                     (const ClipScalars*)out);
+  return hipGetLastError();
+}
 
 int sumsq_spb(uint64_t nseg, uint32_t grad_dtype) {
   // fp16 gradients: 2 segments (16 KiB) per block measured fastest for the

@@ -195,6 +195,28 @@ hipError_t launch_adamw_single_w32(float* w, const float* g, float* m, float* v,
                                    float wd, bool vec, const StepScalars& sc, float beta1,
                                    float beta2, float eps, hipStream_t stream);
 
+// The single-tensor clip (ark_asm_grad_clip, opti.s:369-432): the
+// canonical tree's sum of squares of one fp32 array (one partial per block of
+// two segments, folded past kFinTarget partials), the norm and the clip
+// decision on the device, then the in-place scaling when it clips.
+struct ClipScalars {
+  double sumsq;
+  float norm;      // the pre-clip norm the call reports
+  float coef;      // threshold / norm (1 when not clipped)
+  uint32_t clipped;
+  uint32_t pad;
+};
+static_assert(sizeof(ClipScalars) == 24, "24-byte clip result");
+// Elements one call takes: the partials stay within what one fold and a
+// 1024 x 8-leaf finalize reduce (kFinTarget * kFoldGroup = 2^19 blocks of
+// 2 segments).
+constexpr uint64_t kClipMaxElements = (uint64_t)kFinTarget * kFoldGroup * 2u * kSeg;
+inline uint32_t clip_parts(uint64_t n) { return (uint32_t)((n + 2u * kSeg - 1) / (2u * kSeg)); }
+// parts: clip_parts(n) doubles; folded: ceil(clip_parts(n) / kFoldGroup)
+// doubles (used past kFinTarget partials); out: the decision.  n >= 1.
+hipError_t launch_grad_clip(float* g, uint64_t n, float threshold, double* parts,
+                            double* folded, ClipScalars* out, hipStream_t stream);
+
 hipError_t launch_record_overflow(const ark_opt_hparams& hp,
                                   ark_opt_state* state,
                                   ark_opt_step_info* info, hipStream_t stream);

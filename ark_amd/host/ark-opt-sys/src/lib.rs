@@ -133,6 +133,11 @@ extern "C" {
     pub fn ark_hip_adam_step(w: *mut f32, g: *const f32, m: *mut f32, v: *mut f32, n: u64,
                              lr: f32, beta1: f32, beta2: f32, eps: f32, wd: f32, t: u32,
                              stream: *mut c_void) -> c_int;
+    /// `ark_asm_grad_clip` (`asm/opti.s:369-432`, `src/ffi.rs:111-115`): the
+    /// pre-clip norm into `*norm_out` (a host pointer; the call then waits for
+    /// the stream), grads scaled in place by threshold / norm when it clips.
+    pub fn ark_hip_grad_clip(grads: *mut f32, n: u64, threshold: f32, norm_out: *mut f32,
+                             stream: *mut c_void) -> c_int;
     /// `ark_asm_adam_step_f16` (`asm/opti.s:189-193`, `src/optimizer.rs:20-23`)
     /// plus a stream.
     pub fn ark_hip_adam_step_f16(w: *mut u16, g: *const f32, m: *mut f32, v: *mut f32, n: u64,

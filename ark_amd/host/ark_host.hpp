@@ -16,6 +16,8 @@
 //   Optimizer::record_overflow src/training.rs:228-241
 //   Optimizer::restaurar_momentos  src/optimizer.rs:237-313
 //   CheckpointV3::save_fp16 / load src/io.rs:432-671
+//   grad_clip_global / grad_clip  src/ffi.rs:206-220 (ark_asm_grad_clip,
+//                              asm/opti.s:369-432) over a device buffer
 // Errors: anyhow::Result becomes an ark::host::Error exception carrying the
 // library status and message; the early stop is Error("early_stop_nan")
 // with status ARK_OPT_EARLY_STOP (src/training.rs:236, :300).
@@ -234,6 +236,23 @@ class Optimizer {
   std::vector<TensorRef> tensors_;
   ark_opt_handle* h_ = nullptr;
 };
+
+// src/ffi.rs:206-213: the pre-clip L2 norm of grads[0, n) (device memory),
+// which are scaled in place by threshold / norm when it exceeds threshold;
+// 0 for an empty slice.  Waits for the stream, as the reference returns the
+// norm.
+inline float grad_clip_global(float* grads, uint64_t n, float threshold,
+                              hipStream_t stream = nullptr) {
+  if (n == 0) return 0.0f;
+  float norm = 0.0f;
+  check(ark_hip_grad_clip(grads, n, threshold, &norm, stream));
+  return norm;
+}
+
+// src/ffi.rs:216-220: the reference's alias.
+inline float grad_clip(float* grads, uint64_t n, float threshold, hipStream_t stream = nullptr) {
+  return grad_clip_global(grads, n, threshold, stream);
+}
 
 // src/io.rs:417-671 over device buffers.
 struct CheckpointV3 {

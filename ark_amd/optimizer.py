@@ -121,6 +121,28 @@ def adam_step(w, g, m, v, lr, beta1, beta2, eps, wd, t):
     check(lib().ark_hip_adam_step(wp, gp, mp, vp, n, lr, beta1, beta2, eps, wd, t, st))
 
 
+def grad_clip_global(grads, threshold, wait=True):
+    """ffi.rs:206-213 (grad_clip_global, over ark_asm_grad_clip,
+    opti.s:369-432): the L2 norm of the float32 GPU tensor grads and, when it
+    exceeds threshold, grads scaled in place by threshold / norm
+    (ark_hip_grad_clip), on torch's current stream of its device.  Returns
+    the pre-clip norm (0.0 for an empty tensor, as the reference); with
+    wait=False the work is only queued and None is returned."""
+    import torch
+    if not (grads.is_cuda and grads.is_contiguous() and grads.dtype == torch.float32):
+        raise ValueError("grads must be a contiguous float32 GPU tensor")
+    st = C.c_void_p(torch.cuda.current_stream(grads.device).cuda_stream)
+    norm = C.c_float()
+    check(lib().ark_hip_grad_clip(grads.data_ptr(), grads.numel(), threshold,
+                                  C.byref(norm) if wait else None, st))
+    return norm.value if wait else None
+
+
+def grad_clip(grads, threshold):
+    """ffi.rs:216-220: the reference's alias of grad_clip_global."""
+    return grad_clip_global(grads, threshold)
+
+
 class ParamSet:
     """Parameter-buffer set on one device: fp16 weights, gradients (fp16 or
     fp32, already multiplied by the loss scale), fp32 m and v.  Each array

@@ -841,6 +841,79 @@ def run_dropin(a):
     print(json.dumps(out), flush=True)
 
 
+def run_clip(a):
+    """The drop-in for ark_asm_grad_clip (opti.s:369-432) on the largest
+    gradient its reference wrapper would take, the 24,576,000-value tied
+    embedding of EKO-237M (fp32): calls queued back to back on one stream
+    (no host wait), every one clipping (threshold -1: 0 < norm, so each call
+    scales by -1 / norm and the norm stays 1; 4 B read for the norm, 4 B
+    read and written for the scale = 12 B/value) and, separately, none
+    clipping (4 B/value).  HIP events on the call's stream."""
+    import ctypes as C
+    import torch
+    from ark_amd._lib import check, lib
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    n = 32000 * 768
+    with torch.cuda.stream(stream):
+        g = torch.randn(n, device="cuda") * 1e-3
+    L = lib()
+    sp = C.c_void_p(stream.cuda_stream)
+
+    def timed(thr):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            for _ in range(a.warmup):
+                check(L.ark_hip_grad_clip(g.data_ptr(), n, thr, None, sp))
+            e0.record(stream)
+            for _ in range(a.steps):
+                check(L.ark_hip_grad_clip(g.data_ptr(), n, thr, None, sp))
+            e1.record(stream)
+        stream.synchronize()
+        return e0.elapsed_time(e1) / a.steps
+
+    ms_clip = timed(-1.0)
+    ms_keep = timed(1e30)
+    norm = C.c_float()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        check(L.ark_hip_grad_clip(g.data_ptr(), n, 1e30, C.byref(norm), sp))
+    ms_wait = (time.perf_counter() - t0) * 1e3 / 20
+    cpu = None
+    if not a.no_cpu:
+        import oracle
+        h = g.cpu().numpy().copy()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(a.cpu_seconds, 10.0):
+            oracle.grad_clip_literal(h, -1.0)
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(12 * n * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                   ms_per_call=round(el * 1e3 / reps, 3),
+                   sample=f"{reps} clipping calls of the instruction-by-instruction restatement "
+                          f"of ark_asm_grad_clip (four serial fp32 chains, one thread, as the "
+                          f"reference runs) over the {n}-value embedding gradient in {el:.1f} s")
+    gbs = 12 * n / (ms_clip * 1e-3) / 1e9
+    out = {
+        "metric": "ark_asm_grad_clip drop-in on the EKO-237M embedding gradient, GB/s (1 GPU)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_clip, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"clip: one ark_hip_grad_clip call per step over {n} fp32 values "
+                               "(the tied embedding's gradient), every call clipping",
+                   "params": n, "bytes_per_step": 12 * n,
+                   "ms_per_call_not_clipping": round(ms_keep, 4),
+                   "gbs_not_clipping": round(4 * n / (ms_keep * 1e-3) / 1e9, 2),
+                   "ms_per_call_reporting_the_norm": round(ms_wait, 4)},
+        "roofline": {"kernel": "clip_norm_kernel + clip_scale_kernel", "bound": "hbm",
+                     "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": 12 * n},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -851,11 +924,12 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--path", default="step",
-                    choices=["step", "codec", "ckpt", "grad", "dropin", "ceiling"],
+                    choices=["step", "codec", "ckpt", "grad", "dropin", "ceiling", "clip"],
                     help="step: the optimizer step (headline); codec: the weight codec; "
                          "ckpt: the V4 checkpoint image; grad: the gradient hand-off; "
                          "dropin: the reference's 272 single-tensor calls per step; "
-                         "ceiling: the AdamW pass's access pattern without its arithmetic")
+                         "ceiling: the AdamW pass's access pattern without its arithmetic; "
+                         "clip: the per-tensor clip drop-in on the embedding gradient")
     ap.add_argument("--grad", default="f16", choices=["f16", "f32", "f32-fused"],
                     help="step: gradient type handed to the step (f16 loss-scaled, as the benchmark "
                          "configurations; f32, as the gradient hand-off produces; f32-fused, "
@@ -876,7 +950,7 @@ def main():
         sys.exit(2)
     if a.path != "step":
         {"codec": run_codec, "ckpt": run_ckpt, "grad": run_grad, "dropin": run_dropin,
-         "ceiling": run_ceiling}[a.path](a)
+         "ceiling": run_ceiling, "clip": run_clip}[a.path](a)
         if a.calib_copy:
             calib_copy()
         return

@@ -221,6 +221,24 @@ int ark_opt_get_timing(ark_opt_handle *h, ark_opt_timing *out);
 int ark_hip_adam_step(float *w, const float *g, float *m, float *v, uint64_t n, float lr,
                       float beta1, float beta2, float eps, float wd, uint32_t t, void *stream);
 
+/* Drop-in for ark_asm_grad_clip (opti.s:369-432, declared at ffi.rs:111-115,
+ * wrapped by grad_clip_global at ffi.rs:206-213), the reference's per-tensor
+ * clip (unused by its trainer): the L2 norm of the n fp32 values at grads,
+ * and, when norm > threshold, every value multiplied in place by
+ * threshold / norm (one fp32 division, one fp32 multiply per value).  The
+ * norm is the canonical f64 sum of squares of this header (the tensor taken
+ * alone, without unscaling), rounded to fp32 and square-rooted in fp32:
+ * within 1e-7 relative of the exact norm where the reference's four
+ * sequential fp32 chains drift by up to ~1e-2 at 24.6M values.  An inf value
+ * makes the norm inf (clipping with coefficient 0) and a NaN makes it NaN
+ * (no clipping), as in the reference; the compare is its fcmp / b.le, so an
+ * unordered one does not clip and n = 0 gives norm 0.
+ * norm_out: a host pointer that receives the pre-clip norm (opti.s:423); the
+ * call then waits for the stream, as the reference returns it.  NULL: the
+ * work is only queued.  Workspace (8 bytes per 8192 values, at most
+ * ~4.2 MB) comes from the stream-ordered pool; n <= 2^32. */
+int ark_hip_grad_clip(float *grads, uint64_t n, float threshold, float *norm_out, void *stream);
+
 /* Drop-in for one call of ark_asm_adam_step_f16 (opti.s:189-193, declared
  * at optimizer.rs:20-23 and ffi.rs:105-108): same arguments in the same
  * order, fp32 gradients used as given (no unscale, no clip), t == 0 treated

@@ -87,6 +87,10 @@ def lib():
                                           C.POINTER(_abi.StepInfo)]
     L.ark_ref_amp_replay.argtypes = [C.POINTER(_abi.HParams), C.POINTER(_abi.State), P,
                                      C.c_uint64, P]
+    L.ark_ref_grad_clip_literal.argtypes = [P, C.c_uint64, C.c_float]
+    L.ark_ref_grad_clip_literal.restype = C.c_float
+    L.ark_ref_grad_clip.argtypes = [P, C.c_uint64, C.c_float, C.c_int]
+    L.ark_ref_grad_clip.restype = C.c_float
     L.ark_ref_mix64.argtypes = [C.c_uint64]
     L.ark_ref_mix64.restype = C.c_uint64
     L.ark_ref_splitmix64_next.argtypes = [C.POINTER(C.c_uint64)]
@@ -282,6 +286,21 @@ def amp_replay(hp, state, events):
     scales = np.empty(ev.size, np.float32)
     st = lib().ark_ref_amp_replay(C.byref(hp), C.byref(state), _ptr(ev), ev.size, _ptr(scales))
     return st, scales
+
+
+def grad_clip_literal(g, threshold):
+    """In place on a float32 array: ark_asm_grad_clip (opti.s:369-432)
+    instruction by instruction.  Returns the pre-clip norm."""
+    assert g.dtype == np.float32 and g.flags.c_contiguous
+    return lib().ark_ref_grad_clip_literal(_ptr(g), g.size, threshold)
+
+
+def grad_clip(g, threshold, nthreads=1):
+    """In place on a float32 array: the build's clip (canonical-tree norm,
+    then the reference's compare, division and multiply).  Returns the
+    pre-clip norm."""
+    assert g.dtype == np.float32 and g.flags.c_contiguous
+    return lib().ark_ref_grad_clip(_ptr(g), g.size, threshold, nthreads)
 
 
 def default_hparams():

@@ -720,6 +720,44 @@ int ark_ref_apply_given(const ark_opt_tensor *tab, int32_t nt,
   return ARK_OPT_OK;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Per-tensor clip (opti.s:369-432).                                         */
+/* ------------------------------------------------------------------------ */
+
+/* The clip branch shared by both forms below (opti.s:401-420). */
+static void clip_apply(float *g, uint64_t n, float norm, float thr) {
+  if (!(norm > thr)) return;   /* fcmp s9, s8; b.le .L_clip_skip  :401-402 */
+  const float c = thr / norm;  /* fdiv s17, s8, s9                 :404 */
+  for (uint64_t i = 0; i < n; ++i) g[i] = g[i] * c; /* fmul :412, :418 */
+}
+
+float ark_ref_grad_clip_literal(float *g, uint64_t n, float thr) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}; /* movi v16.4s, #0   :381 */
+  uint64_t i = 0;
+  for (; i + 4 <= n; i += 4)               /* .L_clip_norm4     :384-389 */
+    for (int l = 0; l < 4; ++l)
+      acc[l] = fmaf(g[i + l], g[i + l], acc[l]); /* fmla v16.4s, v0.4s, v0.4s */
+  /* faddp v16.4s, v16.4s, v16.4s; faddp s16, v16.2s  :391-392 */
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  for (; i < n; ++i) s = fmaf(g[i], g[i], s); /* fmadd s16, s0, s0, s16 :396 */
+  const float norm = sqrtf(s);                 /* fsqrt s9, s16         :399 */
+  clip_apply(g, n, norm, thr);
+  return norm;                                 /* fmov s0, s9           :423 */
+}
+
+float ark_ref_grad_clip(float *g, uint64_t n, float thr, int nthreads) {
+  if (n == 0) return 0.0f;
+  ark_opt_tensor t;
+  memset(&t, 0, sizeof(t));
+  t.g = g;
+  t.n = n;
+  int32_t bad = 0;
+  const double sum = ark_ref_sumsq(&t, 1, ARK_OPT_GRAD_F32, 1.0f, nthreads, &bad);
+  const float norm = sqrtf((float)sum);
+  clip_apply(g, n, norm, thr);
+  return norm;
+}
+
 int ark_ref_record_overflow(const ark_opt_hparams *hp, ark_opt_state *st,
                             ark_opt_step_info *info) {
   if (st->early_stop) {

@@ -124,6 +124,19 @@ int ark_ref_amp_replay(const ark_opt_hparams *hp, ark_opt_state *st,
 int ark_ref_record_overflow(const ark_opt_hparams *hp, ark_opt_state *st,
                             ark_opt_step_info *info);
 
+/* ark_asm_grad_clip (opti.s:369-432) restated instruction by instruction:
+ * four fused fp32 chains over the groups of four (lane l takes elements
+ * 4k + l), the faddp pair sums (a0 + a1) + (a2 + a3), the remaining n % 4
+ * values fused in order, fsqrt; when norm > thr (an unordered compare does
+ * not clip) every value times thr / norm.  Returns the pre-clip norm. */
+float ark_ref_grad_clip_literal(float *g, uint64_t n, float thr);
+
+/* The build's definition of the same call (ark_hip_grad_clip): the norm is
+ * sqrtf((float)sum) of the canonical f64 sum of squares of the one tensor
+ * (ark_ref_sumsq, inf and NaN kept in the sum), then the same compare,
+ * division and multiply as the literal form.  n = 0 gives 0. */
+float ark_ref_grad_clip(float *g, uint64_t n, float thr, int nthreads);
+
 /* Synthetic generator of include/ark_synth.h. */
 uint64_t ark_ref_mix64(uint64_t z);
 uint64_t ark_ref_splitmix64_next(uint64_t *state);

@@ -5,8 +5,8 @@
 // step_all calls with the lr_now warmup schedule (optimizer.rs:80-92), an
 // inf gradient that must skip (training.rs:289-305), the logits-gradient
 // overflow (training.rs:228-241), restaurar_momentos (optimizer.rs:237-313),
-// CheckpointV3::save_fp16 / load (io.rs:432-671), and the early stop
-// (training.rs:298-301).  Every step's scalars and every w/m/v bit are
+// CheckpointV3::save_fp16 / load (io.rs:432-671), the early stop
+// (training.rs:298-301) and grad_clip_global (ffi.rs:206-213).  Every step's scalars and every w/m/v bit are
 // compared with the oracle.  Prints "ark_host_test: OK ..." on success.
 #include <stdio.h>
 #include <string.h>
@@ -334,6 +334,27 @@ int main() {
       rejected = err.code() == ARK_OPT_EINVAL;
     }
     EXPECT(rejected, "misaligned table accepted");
+  }
+
+  {  // grad_clip_global (ffi.rs:206-213) on a device slice against the oracle's form of
+     // ark_asm_grad_clip, clipped and not, and the empty slice
+    const uint64_t n = 100003;  // a ragged last block and an n % 4 tail
+    std::vector<float> h(n);
+    ark_ref_synth_normal_f32(h.data(), n, 77, 1, 0, 1e-2f);
+    float* dg = nullptr;
+    hip(hipMalloc(&dg, n * 4), "clip buffer");
+    for (float thr : {0.5f, 1e6f}) {
+      std::vector<float> want = h;
+      const float wn = ark_ref_grad_clip(want.data(), n, thr, 1);
+      hip(hipMemcpy(dg, h.data(), n * 4, hipMemcpyHostToDevice), "clip upload");
+      const float gn = ark::host::grad_clip_global(dg, n, thr);
+      std::vector<float> got(n);
+      hip(hipMemcpy(got.data(), dg, n * 4, hipMemcpyDeviceToHost), "clip read");
+      EXPECT(memcmp(&gn, &wn, 4) == 0, "clip norm %.9g vs oracle %.9g", gn, wn);
+      EXPECT(memcmp(got.data(), want.data(), n * 4) == 0, "clipped values differ (thr %g)", thr);
+    }
+    EXPECT(ark::host::grad_clip(dg, 0, 1.0f) == 0.0f, "empty slice norm not 0");
+    hip(hipFree(dg), "clip free");
   }
 
   printf("ark_host_test: %s (%ld checks, %d failed)\n", g_fail ? "FAIL" : "OK", g_checks, g_fail);

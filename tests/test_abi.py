@@ -170,6 +170,23 @@ def test_single_tensor_dropin_argument_checks():
         assert rc == _abi.EINVAL and "too large" in L.ark_opt_last_error().decode(), n
 
 
+def test_grad_clip_dropin_argument_checks():
+    L = _lib.lib()
+    msg = lambda: L.ark_opt_last_error().decode()
+    norm = C.c_float(7.0)
+    # no values: norm 0 and nothing queued (the Rust wrapper's empty slice)
+    assert L.ark_hip_grad_clip(None, 0, 1.0, C.byref(norm), None) == _abi.OK and norm.value == 0.0
+    assert L.ark_hip_grad_clip(None, 0, 1.0, None, None) == _abi.OK
+    norm.value = 7.0
+    assert L.ark_hip_grad_clip(0x1002, 10, 1.0, C.byref(norm), None) == _abi.EINVAL
+    assert "aligned" in msg() and norm.value == 0.0
+    for n in (2 ** 64 - 1, 2 ** 32 + 1):
+        assert L.ark_hip_grad_clip(0x1000, n, 1.0, None, None) == _abi.EINVAL
+        assert "exceeds" in msg()
+    # aligned and in range: the buffer check (no GPU here) refuses it
+    assert L.ark_hip_grad_clip(0x1000, 10, 1.0, C.byref(norm), None) != _abi.OK
+
+
 def test_synth_argument_checks():
     L = _lib.lib()
     assert L.ark_synth_copy(0x1000, 0x2008, 64, None) == -1
@@ -198,7 +215,7 @@ def test_handle_calls_reject_null():
 def test_headers_cite_reference_interfaces():
     text = open(os.path.join(ROOT, "include", "ark_opt.h")).read()
     for cite in ("opti.s:189-193", "optimizer.rs:171-228", "training.rs:289-326",
-                 "training.rs:228-241", "optimizer.rs:237-313"):
+                 "training.rs:228-241", "optimizer.rs:237-313", "opti.s:369-432"):
         assert cite in text
 
 

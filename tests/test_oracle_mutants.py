@@ -81,6 +81,18 @@ MUTANTS = {
                                        ["grad"]),
     "scatter_in_reverse": ("for (uint32_t i = 0; i < batch_seq; ++i) {",
                            "for (uint32_t i = batch_seq; i-- > 0;) {", ["grad"]),
+    # per-tensor clip (opti.s:369-432)
+    "grad_clip_at_equality": ("if (!(norm > thr)) return;", "if (!(norm >= thr)) return;",
+                              ["grad_clip"]),
+    "grad_clip_coefficient_inverted": ("const float c = thr / norm;",
+                                       "const float c = norm / thr;", ["grad_clip"]),
+    "grad_clip_pairs_folded_in_order": ("float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);",
+                                        "float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];",
+                                        ["grad_clip"]),
+    "grad_clip_tail_unfused": ("for (; i < n; ++i) s = fmaf(g[i], g[i], s);",
+                               "for (; i < n; ++i) s = g[i] * g[i] + s;", ["grad_clip"]),
+    "grad_clip_norm_in_f64": ("const float norm = sqrtf((float)sum);",
+                              "const float norm = (float)sqrt(sum);", ["grad_clip"]),
 }
 PINS = sorted({f for _, _, files in MUTANTS.values() for f in files})
 
