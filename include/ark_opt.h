@@ -229,7 +229,7 @@ int ark_hip_adam_step(float *w, const float *g, float *m, float *v, uint64_t n, 
  * norm is the canonical f64 sum of squares of this header (the tensor taken
  * alone, without unscaling), rounded to fp32 and square-rooted in fp32:
  * within 1e-7 relative of the exact norm where the reference's four
- * sequential fp32 chains drift by up to ~1e-2 at 24.6M values.  An inf value
+ * sequential fp32 chains drift by ~4e-3 at 24.6M values (N(0, 1e-3) data).  An inf value
  * makes the norm inf (clipping with coefficient 0) and a NaN makes it NaN
  * (no clipping), as in the reference; the compare is its fcmp / b.le, so an
  * unordered one does not clip and n = 0 gives norm 0.
