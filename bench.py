@@ -894,6 +894,7 @@ def run_clip(a):
                           f"of ark_asm_grad_clip (four serial fp32 chains, one thread, as the "
                           f"reference runs) over the {n}-value embedding gradient in {el:.1f} s")
     gbs = 12 * n / (ms_clip * 1e-3) / 1e9
+    traffic, tsrc = traffic_from_profiles("eko237m_embed", "clip_kernels")
     out = {
         "metric": "ark_asm_grad_clip drop-in on the EKO-237M embedding gradient, GB/s (1 GPU)",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
@@ -907,8 +908,8 @@ def run_clip(a):
                    "ms_per_call_reporting_the_norm": round(ms_wait, 4)},
         "roofline": {"kernel": "clip_norm_kernel + clip_scale_kernel", "bound": "hbm",
                      "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": 12 * n},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": tsrc, "algorithmic_bytes_per_launch": 12 * n},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
