@@ -117,19 +117,19 @@ def _c3_poke_plan(specs, steps, seed):
     return plan
 
 
-def _c3_sample(specs, ts, seed):
-    """The elements the c3 test follows through every step: every element
-    of gamma_final, of every g1 and g2, and of one seeded 768 x 768 tensor;
-    a seeded strided sample of the embedding (~1.07M) and of every layer's
-    w2 (~38k each, ~1.15M in all).  [(tensor index, element indices)] and
-    the matching oracle HostTensors (their own copies, from `ts`)."""
+def _sample(specs, ts, seed, embed_stride, w2_stride):
+    """The elements a long run follows through every step: every element of
+    gamma_final, of every g1 and g2, and of one seeded d x d tensor; a
+    seeded strided sample of the embedding and of every layer's w2.
+    [(tensor index, element indices)] and the matching oracle HostTensors
+    (their own copies, from `ts`)."""
     rng = np.random.default_rng(seed)
     names = [s.name for s in specs]
     square = [i for i, s in enumerate(specs) if s.name.endswith((".wq", ".wk", ".wv", ".wo"))]
     picks = [(names.index("gamma_final"), None), (int(rng.choice(square)), None)]
     picks += [(i, None) for i, s in enumerate(specs) if s.name.endswith((".g1", ".g2"))]
-    picks.append((names.index("embed"), 23))
-    picks += [(i, 41) for i, s in enumerate(specs) if s.name.endswith(".w2")]
+    picks.append((names.index("embed"), embed_stride))
+    picks += [(i, w2_stride) for i, s in enumerate(specs) if s.name.endswith(".w2")]
     sample, host = [], []
     for i, stride in picks:
         idx = (np.arange(specs[i].n, dtype=np.int64) if stride is None else
@@ -141,31 +141,28 @@ def _c3_sample(specs, ts, seed):
     return sample, host
 
 
-def test_config3_amp_stress_5000_steps_scalars_and_elements():
-    """EKO-237M, 5000 steps from scale 65536 (cap 2^24), gradients fixed from
-    step 0, with the seeded injections of _c3_poke_plan (five random events
-    at this seed, plus the three fixed ones).  Every step's scalars -- skip
-    decision, canonical sum of squares, norm, clip coefficient, inv_scale,
-    lr_eff, t, loss scale and counters -- are checked bit for bit against
-    the oracle's own: its sum of squares over the host copy of the
-    gradients once per distinct loss scale, its finite check over the
-    poked tensors, its state machine (ark_ref_finalize).  The oracle then
-    runs the elementwise update of every applied step, with its own
-    scalars, over the elements of _c3_sample, and after step 5000 those
-    w/m/v elements on the device must equal its bits.  The oracle side runs
-    on a host thread while the device steps."""
+def _long_run(name, steps, seed, sig, scale, plan, strides):
+    """`steps` steps of configuration `name` with its gradients fixed from
+    step 0 and the injections of `plan` ({step: [(tensor, position, fp16
+    bits)]}) planted before each step and removed after it.  Every step's
+    scalars -- skip decision, canonical sum of squares, norm, clip
+    coefficient, inv_scale, lr_eff, t, loss scale and counters -- are
+    compared bit for bit with the oracle's own: its sum of squares over the
+    host copy of the gradients once per distinct loss scale, its finite
+    check over the poked tensors, its state machine (ark_ref_finalize).  The
+    oracle then runs the elementwise update of every applied step, with its
+    own scalars, over the elements of _sample(strides), and after the last
+    step those w/m/v elements on the device must equal its bits.  The oracle
+    side runs on a host thread while the device steps.  Returns the device
+    step infos."""
     import threading
     import torch
-    specs = config_tensors("c3")
-    steps, seed, lr = 5000, 3, HP["lr"]
-    sig = H.log_uniform_sigmas(len(specs), seed)
-    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, 65536.0)
-    cfg, opt = _opt(ps, 65536.0)
-    plan = _c3_poke_plan(specs, steps, 2156)
-    assert sorted(plan) == [15, 287, 813, 1500, 1501, 2100, 2778, 4993]
-    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, 65536.0, nthreads=THREADS)
-    sample, host = _c3_sample(specs, ts, 31)
-    assert sum(idx.size for _, idx in sample) > 2_800_000
+    specs = config_tensors(name)
+    lr = HP["lr"]
+    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, scale)
+    cfg, opt = _opt(ps, scale)
+    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, scale, nthreads=THREADS)
+    sample, host = _sample(specs, ts, 31, *strides)
     ref_info = [None] * steps
     failure = []
 
@@ -184,11 +181,11 @@ def test_config3_amp_stress_5000_steps_scalars_and_elements():
                     sq, bad = oracle.sumsq(poked, _abi.GRAD_F16, 1.0, nthreads=THREADS)
                     assert bad, k
                 else:
-                    scale = float(st.loss_scale)
-                    if scale not in sums:
-                        inv = np.float32(1.0) / np.float32(scale)
-                        sums[scale] = oracle.sumsq(ts, _abi.GRAD_F16, inv, nthreads=THREADS)
-                    sq, bad = sums[scale]
+                    scale_k = float(st.loss_scale)
+                    if scale_k not in sums:
+                        inv = np.float32(1.0) / np.float32(scale_k)
+                        sums[scale_k] = oracle.sumsq(ts, _abi.GRAD_F16, inv, nthreads=THREADS)
+                    sq, bad = sums[scale_k]
                     assert not bad, k
                 _, ri = oracle.finalize(opt.hp, st, sq, bad, lr)
                 if ri.applied:
@@ -216,14 +213,7 @@ def test_config3_amp_stress_5000_steps_scalars_and_elements():
         d = H.info_matches(dev_info[k], ref_info[k])
         assert not d, (k, d)
         assert dev_info[k].applied == (k not in plan), k
-    scales = [i.state.loss_scale for i in dev_info]
-    last = dev_info[-1].state
-    assert last.t == steps - 8 and last.skipped_steps == 8
-    # 65536 halved by the seven skips up to 2778 to 512; 2000 clean steps
-    # later (4778) it doubles to 1024; the skip at 4993 halves it again
-    assert min(scales) == 512.0 and scales[4777] == 512.0 and scales[4778] == 1024.0
-    assert scales[-1] == 512.0
-    assert all(i.clipped for i in dev_info if i.applied)
+    assert sum(idx.size for _, idx in sample) > 2_000_000
     for (i, idx), h in zip(sample, host):
         at = torch.from_numpy(idx).cuda()
         w = H.to_host(ps.w(i)[at])
@@ -233,6 +223,45 @@ def test_config3_amp_stress_5000_steps_scalars_and_elements():
         assert not H.bits_differ32(m, h.m).any(), (specs[i].name, "m")
         assert not H.bits_differ32(v, h.v).any(), (specs[i].name, "v")
     opt.close()
+    return dev_info
+
+
+def test_config3_amp_stress_5000_steps_scalars_and_elements():
+    """EKO-237M, 5000 steps from scale 65536 (cap 2^24), gradients fixed from
+    step 0, with the seeded injections of _c3_poke_plan (five random events
+    at this seed, plus the three fixed ones), through _long_run: every
+    step's scalars against the oracle's own, and after step 5000 gamma_final,
+    every g1/g2, one 768 x 768 tensor and strided samples of the embedding
+    (~1.07M) and of every w2 (~38k each) against the oracle's run of those
+    elements (2.86M in all)."""
+    specs = config_tensors("c3")
+    steps, seed = 5000, 3
+    plan = _c3_poke_plan(specs, steps, 2156)
+    assert sorted(plan) == [15, 287, 813, 1500, 1501, 2100, 2778, 4993]
+    dev_info = _long_run("c3", steps, seed, H.log_uniform_sigmas(len(specs), seed), 65536.0,
+                         plan, (23, 41))
+    scales = [i.state.loss_scale for i in dev_info]
+    last = dev_info[-1].state
+    assert last.t == steps - 8 and last.skipped_steps == 8
+    # 65536 halved by the seven skips up to 2778 to 512; 2000 clean steps
+    # later (4778) it doubles to 1024; the skip at 4993 halves it again
+    assert min(scales) == 512.0 and scales[4777] == 512.0 and scales[4778] == 1024.0
+    assert scales[-1] == 512.0
+    assert all(i.clipped for i in dev_info if i.applied)
+
+
+def test_config4_scaleup_50_steps_scalars_and_elements():
+    """BASELINE c4 as the bench runs it: the 1.3B set (218 tensors,
+    1,279,887,360 params), fp16 gradients N(0, 1e-3) x 65536 fixed from step
+    0, 50 fused steps, through _long_run: every step's scalars against the
+    oracle's own, and after step 50 gamma_final, every g1/g2, one 2048 x 2048
+    tensor and strided samples of the embedding (~1.07M of 65.5M) and of
+    every w2 (~37.6k of 11.3M each) against the oracle's run of those
+    elements (6.3M in all)."""
+    specs = config_tensors("c4")
+    dev_info = _long_run("c4", 50, 7, [1e-3] * len(specs), 65536.0, {}, (61, 300))
+    assert all(i.applied and i.clipped for i in dev_info)
+    assert dev_info[-1].state.t == 50 and dev_info[-1].state.loss_scale == 65536.0
 
 
 def test_state_set_get_and_restaurar_momentos():
