@@ -250,6 +250,20 @@ def test_config3_amp_stress_5000_steps_scalars_and_elements():
     assert all(i.clipped for i in dev_info if i.applied)
 
 
+def test_config2_200_steps_as_the_bench_runs_them():
+    """BASELINE c2 exactly as bench.py builds it (seed 20260501, per-tensor
+    sigma = 10^U(-5,-2) from that seed, loss scale 65536): one fused step
+    repeated 200 times on fixed gradients, through _long_run: every step's
+    scalars against the oracle's own, and after step 200 2.86M sampled
+    elements against the oracle's run of them."""
+    specs = config_tensors("c2")
+    seed = 20260501
+    dev_info = _long_run("c2", 200, seed, H.log_uniform_sigmas(len(specs), seed), 65536.0, {},
+                         (23, 41))
+    assert all(i.applied and i.clipped for i in dev_info)
+    assert dev_info[-1].state.t == 200
+
+
 def test_config4_scaleup_50_steps_scalars_and_elements():
     """BASELINE c4 as the bench runs it: the 1.3B set (218 tensors,
     1,279,887,360 params), fp16 gradients N(0, 1e-3) x 65536 fixed from step
