@@ -971,6 +971,8 @@ int ark_ckpt_v4_pack_plan_create(const ark_ckpt_record* records, int32_t n, int 
   *out = nullptr;
   int rc = check_pack(records, n, with_amp != 0, image, image_bytes);
   if (rc) return rc;
+  int dev = 0;
+  if ((rc = ark::current_device_for(stream, &dev))) return rc;
   ark_ckpt_plan* p = new ark_ckpt_plan();
   if ((rc = build_pack_tables(records, n, p->t))) {
     delete p;
@@ -979,8 +981,8 @@ int ark_ckpt_v4_pack_plan_create(const ark_ckpt_record* records, int32_t n, int 
   p->stream = (hipStream_t)stream;
   p->image = (uint8_t*)image;
   p->with_amp = with_amp != 0;
-  hipError_t e = hipGetDevice(&p->device);
-  if (e == hipSuccess) e = hipMalloc(&p->d_tables, p->t.host.size());
+  p->device = dev;
+  hipError_t e = hipMalloc(&p->d_tables, p->t.host.size());
   if (e == hipSuccess)
     e = hipMemcpy(p->d_tables, p->t.host.data(), p->t.host.size(), hipMemcpyHostToDevice);
   if (e != hipSuccess) {

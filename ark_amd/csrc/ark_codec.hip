@@ -235,7 +235,10 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
       segs.push_back(d);
     }
   }
+  int dev = 0;
+  if ((rc = ark::current_device_for(stream, &dev))) return rc;
   ark_codec_plan* p = new ark_codec_plan();
+  p->device = dev;
   p->stream = (hipStream_t)stream;
   p->direction = direction;
   p->nseg = (uint32_t)segs.size();
@@ -243,8 +246,8 @@ int ark_codec_plan_create(const ark_codec_span* spans, int32_t n_spans, uint32_t
     p->span_dst.push_back(spans[i].dst);
     p->span_bytes.push_back(spans[i].n * ds);
   }
-  hipError_t e = hipGetDevice(&p->device);
-  if (e == hipSuccess && !segs.empty()) {
+  hipError_t e = hipSuccess;
+  if (!segs.empty()) {
     e = hipMalloc(&p->d_segs, segs.size() * sizeof(CodecSeg));
     if (e == hipSuccess)
       e = hipMemcpy(p->d_segs, segs.data(), segs.size() * sizeof(CodecSeg), hipMemcpyHostToDevice);

@@ -74,6 +74,28 @@ int check_buffer_range(const void* p, uint64_t bytes, const char* what, int idx,
 
 }  // namespace
 
+int current_device_for(void* stream, int* dev) {
+  *dev = 0;
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return hip_fail(e, "hipGetDevice");
+  }
+  if (!stream) return ARK_OPT_OK;
+  int sdev = -1;
+  e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return hip_fail(e, "device of the stream");
+  }
+  if (sdev != *dev)
+    return fail(ARK_OPT_EINVAL,
+                "the stream belongs to device %d but device %d is current: make the stream's "
+                "device current before creating the handle or plan",
+                sdev, *dev);
+  return ARK_OPT_OK;
+}
+
 int check_buffer(const void* p, uint64_t bytes, const char* what, int idx) {
   uintptr_t b;
   size_t s;

@@ -43,6 +43,11 @@ class BufferChecker {
   int used_ = 0, next_ = 0;
 };
 
+// The current device, into *dev; when stream is not NULL it must belong to
+// that device (a handle or plan allocates on the current device and launches
+// on its stream), ARK_OPT_EINVAL naming both otherwise.
+int current_device_for(void* stream, int* dev);
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
   int prev = -1;

@@ -865,7 +865,10 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
       segs.push_back(d);
     }
   }
+  int dev = 0;
+  if ((rc = ark::current_device_for(stream, &dev))) return rc;
   ark_grad_plan* p = new ark_grad_plan();
+  p->device = dev;
   p->stream = (hipStream_t)stream;
   p->nseg = (uint32_t)segs.size();
   for (int32_t i = 0; i < n_spans; ++i) {
@@ -873,8 +876,8 @@ int ark_grad_plan_create(const ark_grad_span* spans, int32_t n_spans, void* stre
     p->span_n.push_back(spans[i].n);
     p->span_bytes.push_back(spans[i].n * 4u);
   }
-  hipError_t e = hipGetDevice(&p->device);
-  if (e == hipSuccess) {
+  hipError_t e = hipSuccess;
+  {
     // the no-allocation scatter's set-up on this device (best effort, as in
     // ark_opt_create)
     (void)ark::grad_scratch_prepare(p->device);

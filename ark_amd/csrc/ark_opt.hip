@@ -277,7 +277,7 @@ int ark_opt_create(const ark_opt_tensor* tensors, int32_t n_tensors,
   }
 
   int dev = 0;
-  ARK_HIP(hipGetDevice(&dev));
+  if ((rc = ark::current_device_for(stream, &dev))) return rc;
   // set-up of the no-allocation scatter on this device, so that its first
   // call may come under graph capture (best effort: that call retries it)
   (void)ark::grad_scratch_prepare(dev);

@@ -156,7 +156,9 @@ int ark_opt_default_hparams(ark_opt_hparams *out);
 /* Optimizer::new (optimizer.rs:74) over a parameter-buffer set.  Copies the
  * table and its segment map to the device, allocates the workspace and the
  * device state (t = 0, loss_scale = loss_scale_init), and binds the handle to
- * `stream` on the current device.  One handle per stream; not thread safe.
+ * `stream` on the current device (a stream of another device is refused with
+ * ARK_OPT_EINVAL; so are the plans' creates below).  One handle per stream;
+ * not thread safe.
  * The buffers the step writes (every tensor's w, m and v) must be pairwise
  * disjoint and disjoint from every g, as the reference's distinct per-tensor
  * fields are (memory.rs:202-255); a table that lists a tensor twice or
