@@ -122,3 +122,33 @@ def test_eko237m_gradients_one_call_per_tensor():
         assert np.array_equal(ps.g(i).cpu().numpy().view(np.uint32), want.view(np.uint32)), i
         clipped += wn > 1.0
     assert 0 < clipped < len(specs)
+
+
+def random_case(case):
+    """Seeded random call `case`: sizes from 1 to ~3M values (ragged blocks,
+    n % 4 tails, a few past one 8192-value block), magnitudes 10^U(-30, 15)
+    per call with a spread inside it, thresholds around the norm or special
+    (0, negative, inf, NaN), and now and then an inf or NaN planted.
+    Returns (values, threshold, misalignment in floats)."""
+    rng = np.random.default_rng(9000 + case)
+    r = rng.random()
+    n = (int(rng.integers(1, 9)) if r < 0.15 else int(rng.integers(8185, 8200)) if r < 0.3
+         else int(rng.integers(9, 300000)) if r < 0.8 else int(rng.integers(300000, 3000000)))
+    scale = 10.0 ** rng.uniform(-30, 15)
+    h = (rng.standard_normal(n) * scale * 10.0 ** rng.uniform(-3, 3, n)).astype(F32)
+    if rng.random() < 0.2:
+        h[int(rng.integers(n))] = rng.choice([np.inf, -np.inf, np.nan])
+    probe = oracle.grad_clip(h.copy(), F32(np.inf), nthreads=8)  # the norm, nothing clipped
+    t = rng.random()
+    thr = (float(probe) * float(rng.uniform(0.1, 2.0)) if t < 0.7 and np.isfinite(probe)
+           else float(rng.choice([0.0, -1.0, np.inf, np.nan, 1.0])))
+    return h, thr, int(rng.integers(0, 4))
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_seeded_random_calls(case):
+    """random_case(case) on the device at its misalignment; every result bit
+    against the oracle (tests/test_oracle_grad_clip.py checks on the CPU
+    that the cases reach every outcome)."""
+    h, thr, offset = random_case(case)
+    _check(h, thr, offset=offset)

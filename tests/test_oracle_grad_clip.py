@@ -150,3 +150,23 @@ def test_zero_norm_at_a_zero_threshold_does_not_clip():
     for clip in (oracle.grad_clip, oracle.grad_clip_literal):
         g = np.zeros(9, F32)
         assert clip(g, F32(0.0)) == 0.0 and not np.isnan(g).any()
+
+
+def test_random_device_cases_reach_every_outcome():
+    """The 30 seeded cases tests/test_gpu_grad_clip.py runs on the device,
+    replayed through the oracle: among them calls that clip, calls that do
+    not, an inf norm, a NaN norm, and norms far from 1 either way."""
+    from test_gpu_grad_clip import random_case
+    seen = set()
+    for case in range(30):
+        h, thr, _ = random_case(case)
+        g = h.copy()
+        norm = oracle.grad_clip(g, F32(thr))
+        if np.isnan(norm):
+            seen.add("nan")
+        elif np.isinf(norm):
+            seen.add("inf")
+        else:
+            seen.add("clipped" if norm > F32(thr) else "kept")
+            seen.add("tiny" if norm < 1e-20 else "huge" if norm > 1e10 else "mid")
+    assert {"nan", "inf", "clipped", "kept", "tiny", "huge", "mid"} <= seen, seen
