@@ -74,7 +74,7 @@ def test_config2_full_size_at_a_scale_that_is_not_a_power_of_two():
 
 
 def test_config2_full_size_both_clip_branches():
-    """BASELINE c2's sigma = 10^U(-5,-2) gives a global norm of about 35.8, so
+    """The c2 benchmark's sigma = 10^U(-5,-2) gives a global norm of about 35.8, so
     every c2 step clips.  The same 272-tensor set with those sigmas scaled to
     put the norm at 0.9, 1.1 and 0.95 x grad_clip on three fresh-gradient
     steps takes both branches of optimizer.rs:145-149 (unclipped, clipped,
@@ -251,7 +251,7 @@ def test_config3_amp_stress_5000_steps_scalars_and_elements():
 
 
 def test_config2_200_steps_as_the_bench_runs_them():
-    """BASELINE c2 exactly as bench.py builds it (seed 20260501, per-tensor
+    """Configuration c2 exactly as bench.py builds it (seed 20260501, per-tensor
     sigma = 10^U(-5,-2) from that seed, loss scale 65536): one fused step
     repeated 200 times on fixed gradients, through _long_run: every step's
     scalars against the oracle's own, and after step 200 2.86M sampled
@@ -265,7 +265,7 @@ def test_config2_200_steps_as_the_bench_runs_them():
 
 
 def test_config4_scaleup_50_steps_scalars_and_elements():
-    """BASELINE c4 as the bench runs it: the 1.3B set (218 tensors,
+    """Configuration c4 as the bench runs it: the 1.3B set (218 tensors,
     1,279,887,360 params), fp16 gradients N(0, 1e-3) x 65536 fixed from step
     0, 50 fused steps, through _long_run: every step's scalars against the
     oracle's own, and after step 50 gamma_final, every g1/g2, one 2048 x 2048
