@@ -21,7 +21,8 @@ ORACLE = os.path.join(ROOT, "oracle", "_build", "asan", "libark_oracle.so")
 TESTS = ["tests/test_ckpt_host_parse.py", "tests/test_abi.py", "tests/test_oracle_adam.py",
          "tests/test_oracle_amp.py", "tests/test_oracle_ckpt.py", "tests/test_oracle_clip.py",
          "tests/test_oracle_fp16.py", "tests/test_oracle_grad.py", "tests/test_oracle_norm.py",
-         "tests/test_oracle_vector.py", "tests/test_golden.py", "tests/test_host_ckpt_order.py"]
+         "tests/test_oracle_vector.py", "tests/test_golden.py", "tests/test_host_ckpt_order.py",
+         "tests/test_oracle_grad_clip.py"]
 
 
 def _runtime():
