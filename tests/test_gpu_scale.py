@@ -141,7 +141,7 @@ def _sample(specs, ts, seed, embed_stride, w2_stride):
     return sample, host
 
 
-def _long_run(name, steps, seed, sig, scale, plan, strides):
+def _long_run(name, steps, seed, sig, scale, plan, strides, grad_dtype=_abi.GRAD_F16):
     """`steps` steps of configuration `name` with its gradients fixed from
     step 0 and the injections of `plan` ({step: [(tensor, position, fp16
     bits)]}) planted before each step and removed after it.  Every step's
@@ -153,15 +153,18 @@ def _long_run(name, steps, seed, sig, scale, plan, strides):
     oracle then runs the elementwise update of every applied step, with its
     own scalars, over the elements of _sample(strides), and after the last
     step those w/m/v elements on the device must equal its bits.  The oracle
-    side runs on a host thread while the device steps.  Returns the device
-    step infos."""
+    side runs on a host thread while the device steps.  grad_dtype: fp16
+    (the benchmark configurations) or fp32 gradients (the reference's own
+    type; no injections then).  Returns the device step infos."""
     import threading
     import torch
     specs = config_tensors(name)
     lr = HP["lr"]
-    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, scale)
+    assert grad_dtype == _abi.GRAD_F16 or not plan
+    ps = H.gpu_problem(specs, seed, HP["weight_decay"], sig, scale, grad_dtype=grad_dtype)
     cfg, opt = _opt(ps, scale)
-    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, scale, nthreads=THREADS)
+    ts = H.host_problem(specs, seed, HP["weight_decay"], sig, scale, grad_dtype=grad_dtype,
+                        nthreads=THREADS)
     sample, host = _sample(specs, ts, 31, *strides)
     ref_info = [None] * steps
     failure = []
@@ -184,7 +187,7 @@ def _long_run(name, steps, seed, sig, scale, plan, strides):
                     scale_k = float(st.loss_scale)
                     if scale_k not in sums:
                         inv = np.float32(1.0) / np.float32(scale_k)
-                        sums[scale_k] = oracle.sumsq(ts, _abi.GRAD_F16, inv, nthreads=THREADS)
+                        sums[scale_k] = oracle.sumsq(ts, grad_dtype, inv, nthreads=THREADS)
                     sq, bad = sums[scale_k]
                     assert not bad, k
                 _, ri = oracle.finalize(opt.hp, st, sq, bad, lr)
@@ -260,6 +263,20 @@ def test_config2_200_steps_as_the_bench_runs_them():
     seed = 20260501
     dev_info = _long_run("c2", 200, seed, H.log_uniform_sigmas(len(specs), seed), 65536.0, {},
                          (23, 41))
+    assert all(i.applied and i.clipped for i in dev_info)
+    assert dev_info[-1].state.t == 200
+
+
+def test_config2_fp32_gradients_200_steps():
+    """The c2 set with the reference's own gradient type (fp32,
+    memory.rs:239-243; the step reads 4 B/param for its norm and AdamW):
+    200 steps on fixed gradients N(0, sigma_t) x 65536, through _long_run:
+    every step's scalars against the oracle's own and, after step 200,
+    2.86M sampled elements against the oracle's run of them."""
+    specs = config_tensors("c2")
+    seed = 20260504
+    dev_info = _long_run("c2", 200, seed, H.log_uniform_sigmas(len(specs), seed), 65536.0, {},
+                         (23, 41), grad_dtype=_abi.GRAD_F32)
     assert all(i.applied and i.clipped for i in dev_info)
     assert dev_info[-1].state.t == 200
 
